@@ -1,0 +1,40 @@
+// Shared device helpers for the gfx950 tile kernels: vector types, rounding of float32 to the 16-bit storage
+// formats, and the error slot of the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace krn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Element kinds shared with the host (include/krn_amd.h).
+enum Kind : int { F32 = 0, F16 = 1, BF16 = 2, F8E4M3 = 3, I8 = 4, I32 = 5 };
+
+// float32 -> bfloat16 word, ties to even; a NaN keeps its sign and top payload and is made quiet
+// (the rounding krn's HIP renderer writes, reference compiler/hip.py:123-130).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// float32 -> IEEE half word, round to nearest even (the hardware conversion).
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+}  // namespace krn
+
+// Host side: the last error message of the calling thread, read through krn_amd_last_error().
+void krn_set_error(const char* fmt, ...);
