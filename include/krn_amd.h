@@ -1,0 +1,65 @@
+/* krn_amd.h -- C ABI of libkrn_amd.so, the gfx950 (MI355X) kernel library of krn's tile contraction path.
+ *
+ * Every entry point is host-callable, takes plain device pointers, extents and a hipStream_t passed as void*, enqueues
+ * its work on that stream and returns at once. It returns 0 on success and a nonzero code otherwise, leaving a message
+ * for krn_amd_last_error(). Tensors are row-major and C-contiguous; bf16 is stored as raw uint16 words, fp8 e4m3fn as
+ * uint8 codes (as krn stores them, reference README and tests/compiler/test_tensor_cores.py:305-311).
+ *
+ * These entry points replace what the reference's AMD route left unbuilt: its HIP renderer emitted the source of a
+ * tile kernel (src/krn/compiler/hip.py:20-183) that was compiled only, never loaded or launched, because the backend
+ * module `krn.runtime.hip` named by src/krn/runtime/api.py:324 does not exist. A launch there would have gone through
+ * hipModuleLaunchKernel with krn's generated-kernel ABI (a tensor is a pointer plus one int64 extent per axis,
+ * src/krn/compiler/ir.py:441-452); krn_amd's Python host reaches these entry points through ctypes instead
+ * (krn_amd/runtime/library.py), and still uses hipModuleLaunchKernel for tile programs it compiles with hiprtc.
+ */
+#ifndef KRN_AMD_H
+#define KRN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element kinds. */
+enum krn_kind { KRN_F32 = 0, KRN_F16 = 1, KRN_BF16 = 2, KRN_F8E4M3 = 3, KRN_I8 = 4, KRN_I32 = 5 };
+
+/* Epilogue operations of krn_gemm_nt, applied in order to the float32 accumulator, each rounded to float32:
+ * x * s, x * row[m], x * col[n], x + s, x + row[m], x + col[n]. */
+enum krn_epilogue_op {
+  KRN_MUL_SCALAR = 0, KRN_MUL_ROW = 1, KRN_MUL_COL = 2, KRN_ADD_SCALAR = 3, KRN_ADD_ROW = 4, KRN_ADD_COL = 5
+};
+
+/* C[m, n] = epilogue(sum_k A[m, k] * B[n, k]), A: M x K, B: N x K, C: M x N, all row-major.
+ *
+ * Replaces the tile program `acc = zeros(f32 | i32, bm, bn); for ks in pipelined(K, bk): acc += a[rows, ks] @
+ * b[cols, ks].transpose(); c[rows, cols] = f(acc).to(dtype)` -- krn's Accumulate (reference src/krn/compiler/ir.py:
+ * 309-315, capture rule src/krn/compiler/capture.py:3170-3211) lowered by AMDMFMA.product (src/krn/compiler/hip.py:
+ * 70-97). in_kind: KRN_BF16 / KRN_F16 (float32 accumulation), KRN_F8E4M3 (float32 accumulation; refused by the
+ * reference, src/krn/compiler/matrix.py:129-139) or KRN_I8 (int32 accumulation; refused by the reference capture,
+ * src/krn/compiler/capture.py:3193-3201). out_kind: KRN_F32, KRN_F16, KRN_BF16 (round to nearest even), or KRN_I32
+ * (int8 operands and no epilogue operations only). ops/scalars/vectors: nops <= 4 epilogue operations; vectors[i]
+ * is a device float array of length M (row) or N (column), unused for scalar operations. */
+int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n, int64_t k,
+                int nops, const int* ops, const float* scalars, const float* const* vectors, void* stream);
+
+/* out (cols x rows) = in (rows x cols) transposed, 16-bit elements: turns the B operand of `a[rows, ks] @ b[ks, cols]`
+ * (reference examples/04_libraries/01_gemm_tiles.py:34-40) K-contiguous for krn_gemm_nt. */
+int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream);
+
+/* Flash attention forward: O = softmax(scale-scaled Q K^T, causal-masked if asked) V computed with exp2, for tensors
+ * (bh, sq, d) / (bh, sk, d) of kind KRN_BF16 or KRN_F16, d = 64 or 128, 16-byte aligned. `scale` multiplies the
+ * scores before exp2 (log2(e) / sqrt(d) gives the usual softmax). Replaces krn's flash-attention tile program,
+ * reference examples/04_libraries/08_flash_attention.py:35-59 (causal mask `where(k_pos <= q_pos, s, -1e30)`;
+ * keys past sk are invalid lanes). */
+int krn_attention_fwd(int kind, const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t sq,
+                      int64_t sk, int64_t d, float scale, int causal, void* stream);
+
+/* The message of the calling thread's last failed call. */
+const char* krn_amd_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KRN_AMD_H */

@@ -1,0 +1,227 @@
+"""The CDNA4 (gfx950) lowering of captured tile programs: recognise the contraction programs the hand-written MFMA
+kernels serve, and lower everything else through the generic HIP emitter.
+
+What `lower` returns is a plan the HIP backend launches:
+
+* `GemmPlan`: `acc = zeros(...)`, one K loop of `acc += a[rows, ks] @ b[cols, ks].transpose()` (or `b[ks, cols]`),
+  and one store of an epilogue of `acc` into `c[rows, cols]` -> `krn_gemm_nt` with bf16/f16 (32x32x16 MFMA), fp8
+  e4m3 (32x32x64 f8f6f4 MFMA) or int8 (32x32x32 i8 MFMA) operands. The epilogue may multiply or add float32
+  scalars, per-row vectors (`s[rows, 0:1]`) and per-column vectors (`s[0:1, cols]`), in the program's order, each
+  rounded to float32, then convert to bf16/f16/f32 (or keep int32). The kernel picks its own tile sizes for 256 CUs;
+  the program's `bm, bn, bk` change only the grid it asks for, which must cover the output.
+* `AttentionPlan`: krn's flash-attention tile program (reference examples/04_libraries/08_flash_attention.py:35-59)
+  with head dimension 64 or 128, f16 or bf16, causal or not -> `krn_attention_fwd`.
+* `GenericPlan`: any other tile program -> hipgen (HIP C++ compiled by hiprtc).
+
+Replaces the reference's compile-checked HIP renderer (src/krn/compiler/hip.py:20-183), which emitted 16x16x16
+f16/bf16 MFMA only, refused fp8 (compiler/matrix.py:129-139) and had no int8 product.
+"""
+
+from dataclasses import dataclass, field
+
+from krn_amd.compiler import ir
+from krn_amd.dtypes import BF16, F8E4M3, F16, F32, I8, I32, PY_INT, Dtype
+
+GEMM_OPERANDS = (BF16, F16, F8E4M3, I8)
+
+
+@dataclass(frozen=True)
+class EpilogueOp:
+    """One elementwise step after the product: `op` is "mul" or "add"; the operand is a scalar expression, or a
+    row/column vector read from `tensor` (shape (M, 1) or (1, N))."""
+
+    op: str
+    scalar: ir.Expr | None = None
+    tensor: str | None = None
+    axis: str = ""  # "row" or "col" for a vector
+
+
+@dataclass(frozen=True)
+class GemmPlan:
+    a: str
+    b: str
+    c: str
+    layout: str  # "nt": b is (N, K); "nn": b is (K, N)
+    operand: Dtype
+    output: Dtype
+    ops: tuple[EpilogueOp, ...]
+    bm: int
+    bn: int
+    bk: int
+    loop_extent: ir.Expr
+
+
+@dataclass(frozen=True)
+class AttentionPlan:
+    q: str
+    k: str
+    v: str
+    o: str
+    scale: str
+    dtype: Dtype
+    d: int
+    bq: int
+    causal: bool
+
+
+@dataclass
+class GenericPlan:
+    kernel: ir.Kernel
+    source: str = ""
+    shared: int = 0
+    cache: dict = field(default_factory=dict)
+
+
+def _block_slice(s: ir.SliceExpr, axis: str) -> int | None:
+    """The tile size when `s` is `block.tile`'s slice along grid axis `axis`, else None."""
+    match s:
+        case ir.SliceExpr(start=ir.Binary(op=ir.Op.MUL, lhs=ir.BlockIndex(axis=a), rhs=ir.Const(value=size)),
+                          squeeze=False) if a == axis:
+            return int(size)
+    return None
+
+
+def _k_slice(s: ir.SliceExpr, var: ir.Var, bk: int) -> bool:
+    return isinstance(s.start, ir.Var) and s.start == var and s.extent == bk and not s.squeeze
+
+
+def match_gemm(kernel: ir.Kernel) -> GemmPlan | None:
+    body = kernel.body
+    if len(body) != 3:
+        return None
+    init, loop, store = body
+    if not (isinstance(init, ir.TileAssign) and isinstance(init.value, ir.Zeros)):
+        return None
+    acc = init.var
+    if acc.dtype not in (F32, I32) or len(acc.shape) != 2:
+        return None
+    bm, bn = acc.shape
+    if not (isinstance(loop, ir.For) and len(loop.body) == 1 and isinstance(loop.body[0], ir.Accumulate)):
+        return None
+    if not (isinstance(loop.lo, ir.Const) and loop.lo.value == 0):
+        return None
+    step = loop.body[0]
+    if step.acc != acc:
+        return None
+    bk = loop.step
+    lhs, rhs = step.lhs, step.rhs
+    # A: a[rows, ks]
+    if not (isinstance(lhs, ir.TileLoad) and lhs.tensor.type.rank == 2):
+        return None
+    if _block_slice(lhs.slices[0], "y") != bm or not _k_slice(lhs.slices[1], loop.var, bk):
+        return None
+    # B: b[cols, ks].transpose() or b[ks, cols]
+    if isinstance(rhs, ir.Transpose) and isinstance(rhs.operand, ir.TileLoad) and rhs.operand.tensor.type.rank == 2:
+        load, layout = rhs.operand, "nt"
+        if _block_slice(load.slices[0], "x") != bn or not _k_slice(load.slices[1], loop.var, bk):
+            return None
+    elif isinstance(rhs, ir.TileLoad) and rhs.tensor.type.rank == 2:
+        load, layout = rhs, "nn"
+        if not _k_slice(load.slices[0], loop.var, bk) or _block_slice(load.slices[1], "x") != bn:
+            return None
+    else:
+        return None
+    operand = lhs.dtype
+    if operand != load.dtype or operand not in GEMM_OPERANDS or layout == "nn" and operand not in (BF16, F16):
+        return None
+    if (operand == I8) != (acc.dtype == I32):
+        return None
+    # C: c[rows, cols] = epilogue(acc)
+    if not (isinstance(store, ir.TileStore) and store.tensor.type.rank == 2):
+        return None
+    if _block_slice(store.slices[0], "y") != bm or _block_slice(store.slices[1], "x") != bn:
+        return None
+    value, output = store.value, store.tensor.type.dtype
+    if output not in (F32, F16, BF16, I32):
+        return None
+    if output == I32:
+        if value != acc or acc.dtype != I32:
+            return None
+        ops: list[EpilogueOp] | None = []
+    else:
+        if isinstance(value, ir.Cast) and value.dtype == output and output != F32:
+            value = value.operand
+        ops = _epilogue(value, acc, bm, bn)
+        if ops is None:
+            return None
+    return GemmPlan(lhs.tensor.name, load.tensor.name, store.tensor.name, layout, operand, output, tuple(ops), bm, bn,
+                    bk, loop.hi)
+
+
+def _epilogue(e: ir.Expr, acc: ir.Var, bm: int, bn: int) -> list[EpilogueOp] | None:
+    """The chain of float32 operations from `acc` to `e`, innermost first; None when `e` is not such a chain."""
+    if e == acc:
+        return [] if acc.dtype == F32 else None
+    if isinstance(e, ir.Cast) and e.operand == acc and acc.dtype == I32 and e.dtype == F32:
+        return []
+    if isinstance(e, ir.Binary) and e.op in (ir.Op.MUL, ir.Op.ADD) and e.dtype == F32:
+        for inner, other in ((e.lhs, e.rhs), (e.rhs, e.lhs)):
+            chain = _epilogue(inner, acc, bm, bn)
+            if chain is None:
+                continue
+            operand = _operand(other, bm, bn)
+            if operand is None:
+                continue
+            name = "mul" if e.op is ir.Op.MUL else "add"
+            return [*chain, EpilogueOp(name, *operand)]
+    return None
+
+
+def _operand(e: ir.Expr, bm: int, bn: int) -> tuple | None:
+    """A scalar float32 expression over parameters and constants, or a row/column vector tile load."""
+    if not e.shape:
+        if _scalar_expr(e) and e.dtype == F32:
+            return (e, None, "")
+        return None
+    if isinstance(e, ir.TileLoad) and e.dtype == F32 and e.tensor.type.rank == 2 and len(e.shape) == 2:
+        rows, cols = e.slices
+        if e.shape == (bm, 1) and _block_slice(rows, "y") == bm and isinstance(cols.start, ir.Const) and \
+                cols.start.value == 0 and cols.extent == 1:
+            return (None, e.tensor.name, "row")
+        if e.shape == (1, bn) and _block_slice(cols, "x") == bn and isinstance(rows.start, ir.Const) and \
+                rows.start.value == 0 and rows.extent == 1:
+            return (None, e.tensor.name, "col")
+    return None
+
+
+def _scalar_expr(e: ir.Expr) -> bool:
+    match e:
+        case ir.Const() | ir.Param():
+            return True
+        case ir.Binary(op=op, lhs=a, rhs=b) if op in (ir.Op.MUL, ir.Op.ADD, ir.Op.SUB, ir.Op.DIV):
+            return _scalar_expr(a) and _scalar_expr(b)
+        case ir.Cast(operand=o):
+            return _scalar_expr(o)
+    return False
+
+
+def match_attention(kernel: ir.Kernel) -> AttentionPlan | None:
+    """krn's flash-attention program, recognised by comparing the IR with the canonical program's IR, captured
+    with the same configuration and element types, after renaming every variable and parameter positionally."""
+    from krn_amd.compiler import programs
+
+    tensors = [(n, t) for n, t in kernel.params if isinstance(t, ir.TensorType)]
+    scalars = [(n, t) for n, t in kernel.params if not isinstance(t, ir.TensorType)]
+    if len(tensors) != 4 or len(scalars) != 1 or any(t.rank != 3 for _, t in tensors):
+        return None
+    dtype = tensors[0][1].dtype
+    if dtype not in (F16, BF16) or any(t.dtype != dtype for _, t in tensors) or scalars[0][1] != F32:
+        return None
+    consts = dict(kernel.consts)
+    if len(consts) != 1:
+        return None
+    values = dict(next(iter(consts.values())))
+    if set(values) != {"bq", "bk", "d", "causal"} or values["d"] not in (64, 128):
+        return None
+    canonical = programs.attention(values, dtype)
+    if programs.canonical_form(kernel) != programs.canonical_form(canonical):
+        return None
+    names = [n for n, _ in kernel.params]
+    return AttentionPlan(names[0], names[1], names[2], names[3], names[4], dtype, int(values["d"]),
+                         int(values["bq"]), bool(values["causal"]))
+
+
+def lower(kernel: ir.Kernel) -> GemmPlan | AttentionPlan | GenericPlan:
+    """The plan for `kernel` on gfx950: a hand-written MFMA kernel when the program is one they serve, otherwise
+    the generic HIP lowering."""
+    return match_gemm(kernel) or match_attention(kernel) or GenericPlan(kernel)

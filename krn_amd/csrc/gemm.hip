@@ -384,3 +384,42 @@ int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind
 }
 
 }  // extern "C"
+
+// out[c, r] = in[r, c] for 16-bit elements, through a 64x65-word LDS tile: the B operand of a `b[ks, cols]`
+// product is turned K-contiguous before the NT main loop reads it.
+__global__ __launch_bounds__(256) void transpose16(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
+                                                   int64_t rows, int64_t cols) {
+  __shared__ uint16_t tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    tile[i][tx] = (r < rows && c < cols) ? in[r * cols + c] : 0;
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t c = c0 + i, r = r0 + tx;
+    if (c < cols && r < rows) out[c * rows + r] = tile[tx][i];
+  }
+}
+
+extern "C" int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols < 0) {
+    krn_set_error("transpose: negative extent");
+    return -1;
+  }
+  if (rows == 0 || cols == 0) return 0;
+  const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
+  if (gx > 0x7fffffff || gy > 65535) {
+    krn_set_error("transpose: %lld x %lld exceeds the grid limit", (long long)rows, (long long)cols);
+    return -1;
+  }
+  hipLaunchKernelGGL(transpose16, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)in, (uint16_t*)out, rows, cols);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    krn_set_error("transpose launch: %s", hipGetErrorString(err));
+    return (int)err;
+  }
+  return 0;
+}

@@ -1,0 +1,485 @@
+"""The AMD backend of the runtime contract: gfx950 devices, streams, events, tensors and tile-kernel launches.
+
+`MODULES["amd"]` names this module (reference src/krn/runtime/api.py:321-326, where the module was missing); it
+exposes `BACKEND`. Host code is Python over ctypes: the HIP runtime (`libamdhip64`) for memory, streams and events,
+the kernel library `libkrn_amd.so` for the hand-written MFMA kernels, and hiprtc plus the HIP module API for tile
+programs the generic lowering compiles. The shape follows the CUDA backend of the reference
+(src/krn/runtime/cuda_backend.py): a tensor owns its allocation, a launch plans once per signature, an event is settled
+by a waiter thread, never by a host callback.
+"""
+
+import asyncio
+import ctypes
+import hashlib
+import inspect
+import threading
+from collections.abc import Callable, Sequence
+from ctypes import c_float, c_int, c_int64, c_void_p
+from dataclasses import is_dataclass
+from pathlib import Path
+
+import numpy as np
+
+from krn_amd import dtypes as D
+from krn_amd.compiler import cdna4, hipgen, space
+from krn_amd.compiler import ir
+from krn_amd.compiler.capture import capture
+from krn_amd.dtypes import BF16, F32, Dtype
+from krn_amd.frontend import Blocks, Kernel, Tensor, const_fields
+from krn_amd.runtime import api, hipapi, library
+from krn_amd.runtime.api import Backend, Bound, Device, Event, Graph, Launcher, Stream, current_stream
+
+TARGET = "gfx950"
+HIPRTC_OPTIONS = [f"--offload-arch={TARGET}", "-O3", "-std=c++17", "-ffp-contract=off"]
+
+
+class HIPEvent(Event):
+    """A hipEvent recorded on a stream. Completion is observed by a waiter thread that blocks in
+    hipEventSynchronize, so subscribers run on that thread."""
+
+    def __init__(self, device: "HIPDevice", handle: int) -> None:
+        self.device, self.handle = device, handle
+        self._callbacks: list[Callable[[], None]] = []
+        self._done = False
+        self._error: BaseException | None = None
+        self._lock = threading.Lock()
+        self._thread: threading.Thread | None = None
+
+    def done(self) -> bool:
+        if self._done:
+            return True
+        code = hipapi.api().lib.hipEventQuery(c_void_p(self.handle))
+        if code == 0:
+            self._done = True
+        elif code != 600:  # hipErrorNotReady
+            self._done, self._error = True, hipapi.HIPError("hipEventQuery", code, "error", "device work failed")
+        return self._done
+
+    def wait(self, timeout: float | None = None) -> None:
+        try:
+            hipapi.api().hipEventSynchronize(c_void_p(self.handle))
+        except hipapi.HIPError as error:
+            self._error = error
+        self._done = True
+
+    def _waiter(self) -> None:
+        self.wait()
+        with self._lock:
+            callbacks, self._callbacks = self._callbacks, []
+        for callback in callbacks:
+            callback()
+
+    def subscribe(self, callback: Callable[[], None]) -> bool:
+        with self._lock:
+            if self._done:
+                return True
+            self._callbacks.append(callback)
+            if self._thread is None:
+                self._thread = threading.Thread(target=self._waiter, daemon=True)
+                self._thread.start()
+        return False
+
+    @property
+    def error(self) -> BaseException | None:
+        return self._error
+
+    def elapsed_since(self, earlier: Event) -> float:
+        if not isinstance(earlier, HIPEvent):
+            raise TypeError("elapsed time is measured between two HIP events")
+        return hipapi.elapsed_ms(earlier.handle, self.handle)
+
+    def __del__(self) -> None:
+        try:
+            if self._thread is None or not self._thread.is_alive():
+                hipapi.api().lib.hipEventDestroy(c_void_p(self.handle))
+        except Exception:
+            pass
+
+
+class HIPStream(Stream):
+    def __init__(self, device: "HIPDevice", handle: int) -> None:
+        self.device, self.handle = device, handle
+        self._pending: list[tuple[str, HIPEvent | None]] = []
+        self._keep: list[tuple[object, ...]] = []
+
+    def record(self) -> HIPEvent:
+        event = HIPEvent(self.device, hipapi.event_create())
+        hipapi.api().hipEventRecord(c_void_p(event.handle), c_void_p(self.handle))
+        return event
+
+    def wait(self, event: Event) -> None:
+        if not isinstance(event, HIPEvent):
+            raise TypeError("a HIP stream waits for HIP events")
+        hipapi.api().hipStreamWaitEvent(c_void_p(self.handle), c_void_p(event.handle), 0)
+
+    def pending_launches(self) -> tuple[str, ...]:
+        return tuple(name for name, _ in self._pending)
+
+    def note(self, name: str, keep: tuple[object, ...]) -> None:
+        """Remember a launch and hold its arguments until the stream is next synchronized."""
+        self._pending.append((name, None))
+        self._keep.append(keep)
+
+    def sync(self) -> None:
+        hipapi.api().hipStreamSynchronize(c_void_p(self.handle))
+        self._pending.clear()
+        self._keep.clear()
+
+
+class HIPTensor(Tensor):
+    """C-contiguous device memory with its element type (bf16 as uint16 words, fp8 as uint8 codes) and shape."""
+
+    def __init__(self, device: "HIPDevice", pointer: int, dtype: Dtype, shape: tuple[int, ...], owner=None) -> None:
+        self.device, self.pointer, self.dtype, self.shape = device, pointer, dtype, tuple(int(s) for s in shape)
+        self.numpy = D.NUMPY[dtype]
+        self._owner = owner  # a view keeps the owner alive; an owner frees its memory
+
+    @property
+    def nbytes(self) -> int:
+        return self.numpy.itemsize * int(np.prod(self.shape))
+
+    def to_host(self, stream: HIPStream | None = None) -> np.ndarray:
+        """A numpy copy, after the work queued on `stream` (default: the current stream) has run."""
+        stream = stream or self.device.launch_stream()
+        array = np.empty(self.shape, self.numpy)
+        if array.nbytes:
+            hipapi.api().hipMemcpyAsync(c_void_p(array.ctypes.data), c_void_p(self.pointer), array.nbytes,
+                                        hipapi.D2H, c_void_p(stream.handle))
+        stream.sync()
+        return array
+
+    def copy_from(self, array: np.ndarray, stream: HIPStream | None = None) -> None:
+        stream = stream or self.device.launch_stream()
+        data = np.ascontiguousarray(array, dtype=self.numpy)
+        if data.shape != self.shape:
+            raise ValueError(f"shape {data.shape} does not match the tensor's {self.shape}")
+        if data.nbytes:
+            hipapi.api().hipMemcpyAsync(c_void_p(self.pointer), c_void_p(data.ctypes.data), data.nbytes, hipapi.H2D,
+                                        c_void_p(stream.handle))
+        stream.sync()
+
+    def __repr__(self) -> str:
+        return f"HIPTensor({self.dtype}{list(self.shape)} at {self.pointer:#x})"
+
+    def __del__(self) -> None:
+        if self._owner is None and self.pointer:
+            try:
+                hipapi.free(self.pointer)
+            except Exception:
+                pass
+            self.pointer = 0
+
+
+def _kind(argument: object) -> object:
+    """What compiling depends on in one argument."""
+    if isinstance(argument, HIPTensor):
+        return ("tensor", argument.dtype, len(argument.shape))
+    if is_dataclass(argument) and not isinstance(argument, type):
+        return ("config", type(argument).__name__, tuple(sorted(const_fields(argument).items())))
+    return ("scalar", type(argument).__name__)
+
+
+class Program:
+    """A hiprtc-compiled module with one entry point."""
+
+    def __init__(self, source: str, entry: str, scratch: int = 0) -> None:
+        self.source, self.entry, self.scratch = source, entry, scratch
+        self.code = hipapi.rtc().compile(source, entry, HIPRTC_OPTIONS)
+        module = c_void_p()
+        buffer = ctypes.create_string_buffer(self.code, len(self.code))
+        hipapi.api().hipModuleLoadData(ctypes.byref(module), buffer)
+        function = c_void_p()
+        hipapi.api().hipModuleGetFunction(ctypes.byref(function), module, entry.encode())
+        self.module, self.function, self._buffer = module, function, buffer
+
+    def launch(self, grid: tuple[int, int, int], threads: int, params: list, stream: int) -> None:
+        pointers = (c_void_p * max(len(params), 1))(*(ctypes.cast(ctypes.byref(p), c_void_p) for p in params))
+        hipapi.api().hipModuleLaunchKernel(self.function, grid[0], grid[1], grid[2], threads, 1, 1, 0,
+                                           c_void_p(stream), pointers, None)
+
+
+_programs: dict[str, Program] = {}
+_programs_lock = threading.Lock()
+
+
+def generic_program(kernel: ir.Kernel) -> Program:
+    entry = f"krn_{kernel.name}"
+    source, scratch = hipgen.emit(kernel, entry)
+    digest = hashlib.sha256(source.encode()).hexdigest()
+    with _programs_lock:
+        if digest not in _programs:
+            _programs[digest] = Program(source, entry, scratch)
+        return _programs[digest]
+
+
+class Launch:
+    """One planned launch of one signature: the captured IR, its gfx950 plan, and how to run it."""
+
+    def __init__(self, kernel: ir.Kernel, plan) -> None:
+        self.kernel, self.plan = kernel, plan
+
+    def run(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
+        params = dict(zip((name for name, _ in self.kernel.params), values))
+        plan = self.plan
+        if isinstance(plan, cdna4.GemmPlan) and self._gemm(plan, params, grid, stream):
+            return
+        if isinstance(plan, cdna4.AttentionPlan) and self._attention(plan, params, grid, stream):
+            return
+        self._generic(values, grid, stream)
+
+    def _gemm(self, plan: cdna4.GemmPlan, params: dict, grid: Blocks, stream: HIPStream) -> bool:
+        a, b, c = params[plan.a], params[plan.b], params[plan.c]
+        m, k = a.shape
+        n = b.shape[0] if plan.layout == "nt" else b.shape[1]
+        kb = b.shape[1] if plan.layout == "nt" else b.shape[0]
+        extent = space.extent(plan.loop_extent, params) if isinstance(plan.loop_extent, ir.Dim) else None
+        if extent != k or kb != k or c.shape != (m, n) or (grid.x, grid.y, grid.z) != (
+                -(-n // plan.bn), -(-m // plan.bm), 1):
+            return False  # not the whole product: the generic lowering keeps the program's exact meaning
+        ops = []
+        for op in plan.ops:
+            base = library.MUL_SCALAR if op.op == "mul" else library.ADD_SCALAR
+            if op.tensor is None:
+                ops.append((base, float(_scalar_value(op.scalar, params)), 0))
+            else:
+                vector = params[op.tensor]
+                want = (m, 1) if op.axis == "row" else (1, n)
+                if vector.shape != want:
+                    return False
+                ops.append((base + (1 if op.axis == "row" else 2), 0.0, vector.pointer))
+        if plan.layout == "nn":
+            scratch = self.device_scratch(stream, n * k * 2)
+            library.transpose16(b.pointer, scratch.pointer, k, n, stream.handle)
+            library.gemm_nt(plan.operand, a.pointer, scratch.pointer, c.pointer, plan.output, m, n, k, ops,
+                            stream.handle)
+            stream.note(self.kernel.name, (scratch,))
+        else:
+            library.gemm_nt(plan.operand, a.pointer, b.pointer, c.pointer, plan.output, m, n, k, ops, stream.handle)
+        return True
+
+    def device_scratch(self, stream: HIPStream, nbytes: int) -> HIPTensor:
+        return stream.device.empty(D.U8, max(nbytes, 1))
+
+    def _attention(self, plan: cdna4.AttentionPlan, params: dict, grid: Blocks, stream: HIPStream) -> bool:
+        q, k, v, o = (params[n] for n in (plan.q, plan.k, plan.v, plan.o))
+        bh, sq, d = q.shape
+        sk = k.shape[1]
+        if d != plan.d or k.shape != (bh, sk, d) or v.shape != (bh, sk, d) or o.shape != (bh, sq, d):
+            return False
+        if (grid.x, grid.y, grid.z) != (-(-sq // plan.bq), bh, 1):
+            return False
+        library.attention_fwd(plan.dtype, q.pointer, k.pointer, v.pointer, o.pointer, bh, sq, sk, d,
+                              float(np.float32(params[plan.scale])), plan.causal, stream.handle)
+        return True
+
+    def _generic(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
+        program = generic_program(self.kernel)
+        params: list = []
+        for (name, kind), value in zip(self.kernel.params, values):
+            if isinstance(kind, ir.TensorType):
+                if not isinstance(value, HIPTensor) or len(value.shape) != kind.rank:
+                    raise TypeError(f"{self.kernel.name}: `{name}` needs a rank-{kind.rank} device tensor")
+                params.append(c_void_p(value.pointer))
+                params.extend(c_int64(s) for s in value.shape)
+            elif kind.is_float:
+                params.append(ctypes.c_double(value) if kind.bits == 64 else c_float(value))
+            elif kind.bits == 64:
+                params.append(c_int64(int(value)))
+            elif kind.bits == 8:
+                params.append(ctypes.c_uint8(int(value)) if kind.kind.value == "uint" else ctypes.c_int8(int(value)))
+            else:
+                params.append(c_int(int(value)))
+        blocks = grid.x * grid.y * grid.z
+        if blocks == 0:
+            return
+        if program.scratch:
+            scratch = stream.device.empty(D.U8, blocks * program.scratch)
+            params.append(c_void_p(scratch.pointer))
+            stream.note(self.kernel.name, (scratch,))
+        program.launch((grid.x, grid.y, grid.z), hipgen.THREADS, params, stream.handle)
+
+
+def _scalar_value(e: ir.Expr, params: dict) -> np.float32:
+    """A float32 scalar epilogue operand, evaluated as the kernel would: each operation rounded to float32."""
+    match e:
+        case ir.Const(value=v):
+            return np.float32(v)
+        case ir.Param(name=n):
+            return np.float32(params[n])
+        case ir.Cast(operand=o):
+            return np.float32(_scalar_value(o, params))
+        case ir.Binary(op=op, lhs=a, rhs=b):
+            x, y = _scalar_value(a, params), _scalar_value(b, params)
+            with np.errstate(all="ignore"):
+                return np.float32({ir.Op.MUL: np.multiply, ir.Op.ADD: np.add, ir.Op.SUB: np.subtract,
+                                   ir.Op.DIV: np.divide}[op](x, y))
+    raise ValueError(f"{type(e).__name__} is not a scalar epilogue operand")
+
+
+class HIPLauncher(Launcher):
+    """A kernel with an optional explicit geometry. The first call of a signature captures and plans it."""
+
+    def __init__(self, device: "HIPDevice", kernel: Kernel, launch: Blocks | None) -> None:
+        self.device, self.kernel, self.launch = device, kernel, launch
+        self.parameters = tuple(inspect.signature(kernel.fn).parameters)
+        self._plans: dict[tuple, Launch] = {}
+        self._lock = threading.Lock()
+
+    def ordered(self, args: tuple, kwargs: dict) -> tuple:
+        if not kwargs and len(args) == len(self.parameters):
+            return args
+        try:
+            ordered = (*args, *(kwargs.pop(name) for name in self.parameters[len(args):]))
+        except KeyError as missing:
+            raise TypeError(f"{self.kernel.name}() is missing the argument {missing}") from None
+        if kwargs or len(ordered) != len(self.parameters):
+            raise TypeError(f"{self.kernel.name}() takes {len(self.parameters)} arguments")
+        return ordered
+
+    def plan(self, args: Sequence[object]) -> Launch:
+        signature = tuple(map(_kind, args))
+        try:
+            return self._plans[signature]
+        except KeyError:
+            pass
+        with self._lock:
+            if signature not in self._plans:
+                consts = {n: const_fields(a) for n, a in zip(self.parameters, args)
+                          if is_dataclass(a) and not isinstance(a, type)}
+                dtypes = {n: a.dtype for n, a in zip(self.parameters, args) if isinstance(a, HIPTensor)}
+                path = Path(inspect.getsourcefile(self.kernel.fn))
+                kernel = capture(path, self.kernel.name, consts=consts, dtypes=dtypes)
+                self._plans[signature] = Launch(kernel, cdna4.lower(kernel))
+            return self._plans[signature]
+
+    def encode(self, args: tuple) -> Callable[[HIPStream], None]:
+        launch = self.plan(args)
+        values = space.runtime_args(launch.kernel, args)
+        grid = self.launch if self.launch is not None else space.geometry(launch.kernel, values)
+
+        def run(stream: HIPStream) -> None:
+            launch.run(values, grid, stream)
+            stream.note(self.kernel.name, tuple(values))
+
+        return run
+
+    def __call__(self, *args, **kwargs) -> None:
+        self.encode(self.ordered(args, kwargs))(self.device.launch_stream())
+
+    def submit(self, *args, **kwargs) -> HIPEvent:
+        stream = self.device.launch_stream()
+        self.encode(self.ordered(args, kwargs))(stream)
+        return stream.record()
+
+    def bind(self, *args, **kwargs) -> "HIPBound":
+        return HIPBound(self, self.ordered(args, kwargs))
+
+    def explain(self, *args, **kwargs) -> dict:
+        launch = self.plan(self.ordered(args, kwargs))
+        return {"kernel": launch.kernel.name, "target": TARGET, "plan": type(launch.plan).__name__,
+                "detail": repr(launch.plan) if not isinstance(launch.plan, cdna4.GenericPlan) else "hipgen"}
+
+
+class HIPBound(Bound):
+    def __init__(self, launcher: HIPLauncher, args: tuple) -> None:
+        self.launcher = launcher
+        self.rebind(*args)
+
+    def rebind(self, *args, **kwargs) -> None:
+        self.run = self.launcher.encode(self.launcher.ordered(args, kwargs))
+
+    def __call__(self) -> None:
+        self.run(self.launcher.device.launch_stream())
+
+    def submit(self) -> HIPEvent:
+        stream = self.launcher.device.launch_stream()
+        self.run(stream)
+        return stream.record()
+
+
+class HIPGraph(Graph):
+    """Recorded launches replayed in order by one call. The launches are re-issued from their prebound form."""
+
+    def __init__(self, device: "HIPDevice", fn: Callable, args: tuple, kwargs: dict) -> None:
+        self.device, self.fn = device, fn
+        self.args, self.kwargs = args, kwargs
+        fn(*args, **kwargs)
+
+    def __call__(self, *args, **kwargs) -> None:
+        self.fn(*(args or self.args), **(kwargs or self.kwargs))
+
+    def submit(self, *args, **kwargs) -> HIPEvent:
+        self(*args, **kwargs)
+        return self.device.launch_stream().record()
+
+
+class HIPDevice(Device):
+    """One gfx950 GPU."""
+
+    def __init__(self, arch: str, ordinal: int = 0) -> None:
+        if hipapi.device_count() == 0:
+            raise api.BackendUnavailable("no HIP device is visible to this process")
+        self.arch, self.ordinal = arch, ordinal
+        hipapi.api().hipSetDevice(ordinal)
+        library.lib()  # the kernel library must be present: there is no fallback path
+        self._default = HIPStream(self, hipapi.stream_create())
+        self._streams: list[HIPStream] = [self._default]
+
+    @property
+    def default_stream(self) -> HIPStream:
+        return self._default
+
+    def launch_stream(self) -> HIPStream:
+        stream = current_stream.get()
+        return stream if isinstance(stream, HIPStream) else self._default
+
+    def stream(self) -> HIPStream:
+        created = HIPStream(self, hipapi.stream_create())
+        self._streams.append(created)
+        return created
+
+    def empty(self, dtype, *shape: int) -> HIPTensor:
+        element = D.of(dtype)
+        count = int(np.prod(shape)) if shape else 1
+        pointer = hipapi.malloc(count * D.NUMPY[element].itemsize)
+        return HIPTensor(self, pointer, element, shape)
+
+    def to_device(self, array: np.ndarray, dtype=None) -> HIPTensor:
+        """A device copy of a host array. bf16 and fp8 arrays pass their element type (`T.bf16`, `T.f8e4m3fn`)."""
+        array = np.ascontiguousarray(array)
+        element = D.of(dtype) if dtype is not None else D.FROM_NUMPY[array.dtype]
+        if array.dtype != D.NUMPY[element]:
+            raise TypeError(f"a {element} tensor is stored as {D.NUMPY[element]}, got {array.dtype}")
+        tensor = self.empty(element, *array.shape)
+        tensor.copy_from(array)
+        return tensor
+
+    def launcher(self, kernel: Kernel, launch=None) -> HIPLauncher:
+        return HIPLauncher(self, kernel, launch)
+
+    def graph(self, fn: Callable, *args, **kwargs) -> HIPGraph:
+        return HIPGraph(self, fn, args, kwargs)
+
+    def sync(self) -> None:
+        for stream in self._streams:
+            stream.sync()
+
+    async def synchronize(self) -> None:
+        await asyncio.get_running_loop().run_in_executor(None, self.sync)
+
+
+class HIPBackend(Backend):
+    vendor = "amd"
+
+    def __init__(self) -> None:
+        self._devices: dict[str, HIPDevice] = {}
+
+    def device(self, arch: str) -> HIPDevice:
+        if arch != TARGET:
+            raise api.BackendUnavailable(f"the AMD backend serves {TARGET}, not {arch}")
+        if arch not in self._devices:
+            self._devices[arch] = HIPDevice(arch)
+        return self._devices[arch]
+
+
+BACKEND = HIPBackend()

@@ -155,7 +155,7 @@ class Emitter:
                     params.append(f"{ctype(dtype if dtype != I64 else PY_INT)} {slot}")
         params += ["long long gx", "long long gy", "long long gz", "long long first", "long long last"]
         total = sum(self.size(c) * n for _, c, n in self.buffers)
-        head = [PRELUDE, f"void {self.kernel.name}({', '.join(params)}) {{"]
+        head = [PRELUDE, f"void krn_{self.kernel.name}({', '.join(params)}) {{"]
         head.append(f"    char* _arena = (char*)aligned_alloc(64, {max(64, (total + len(self.buffers) * 64 + 63) // 64 * 64)});")
         offset = 0
         for name, c, n in self.buffers:
@@ -472,7 +472,7 @@ class Program:
     def __init__(self, kernel: ir.Kernel) -> None:
         self.kernel = kernel
         self.library, self.source = compile_kernel(kernel)
-        self.function = getattr(self.library, kernel.name)
+        self.function = getattr(self.library, f"krn_{kernel.name}")
         self.function.restype = None
 
     def arguments(self, args: Sequence[object]) -> list[object]:
