@@ -220,3 +220,12 @@ def matmul_f32(t: Tiling, a: Matrix[T.f32], b: Matrix[T.f32], c: Matrix[T.f32]) 
     for ks in pipelined(a.shape[1], t.bk):
         acc += a[rows, ks] @ b[ks, cols]
     c[rows, cols] = acc
+
+
+@kernel
+def matmul_f16_f32(t: Tiling, a: Matrix[T.f16], b: Matrix[T.f16], c: Matrix[T.f32]) -> None:
+    rows, cols = block.tile(t.bm, t.bn)
+    acc = zeros(T.f32, t.bm, t.bn)
+    for ks in pipelined(a.shape[1], t.bk):
+        acc += a[rows, ks] @ b[ks, cols]
+    c[rows, cols] = acc
