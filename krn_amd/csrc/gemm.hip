@@ -3,8 +3,9 @@
 // This is the lowering of krn's tile contraction `acc += a[rows, ks] @ b[cols, ks].transpose()` followed by
 // `c[rows, cols] = f(acc).to(dtype)` (reference compiler/ir.py:309-315 Accumulate, compiler/emit.py:788-821). One
 // workgroup owns a BM x BN output tile, four waves split it 2 x 2, and every wave keeps its accumulators in
-// registers as 32x32 MFMA blocks. The K loop stages 128-byte slices of both operands through LDS, double buffered:
-// the global loads of slice k+1 are in flight while the MFMAs of slice k run.
+// registers as 32x32 MFMA blocks. Two main loops: `gemm_pipe` for whole 256 x 256 tiles (a ring of direct-to-LDS
+// slices, see there) and `gemm_tile` for ragged shapes (128-byte slices staged through registers, bounds-checked,
+// double buffered). Both end in the same epilogue, `store_block`.
 //
 // One byte-oriented main loop serves three operand formats, because each MFMA consumes the same 16 bytes per lane
 // per half-wave:
@@ -14,8 +15,8 @@
 // The K order inside one instruction is the hardware's; A and B fragments are read with the same byte layout, so
 // every lane pairs A[m, k] with B[n, k] for the same k.
 //
-// LDS layout: a tile row is 128 bytes = 8 chunks of 16 bytes; chunk c of row r lives at slot c ^ (r & 7), so the
-// 16-byte fragment reads of 8 consecutive rows touch 8 different bank groups (no conflicts).
+// LDS layout: a tile row of a K slice is 64 or 128 bytes (4 or 8 chunks of 16 bytes), swizzled per row so that
+// the 16-byte fragment reads of 16 consecutive rows hit distinct banks (swz4 / swz8 below).
 #include <type_traits>
 
 #include "common.h"
@@ -82,41 +83,92 @@ struct Mfma<FMT_FP8> {
   }
 };
 
-__device__ __forceinline__ float apply_ops(float v, const Epilogue& e, int64_t m, int64_t n) {
-  for (int i = 0; i < e.nops; ++i) {
-    float s;
-    switch (e.op[i] % 3) {
-      case 0: s = e.scalar[i]; break;
-      case 1: s = e.vec[i][m]; break;
-      default: s = e.vec[i][n]; break;
-    }
-    v = e.op[i] < 3 ? __fmul_rn(v, s) : __fadd_rn(v, s);
-  }
-  return v;
-}
+// Store one 32x32 accumulator block (the C layout of a 32x32 MFMA: lane holds column lane & 31 and rows
+// (r/4)*8 + (lane/32)*4 + r%4) through a per-wave LDS patch with a 36-word row stride, so that each lane then owns
+// 16 consecutive elements of one row: lane l takes row l/2, columns (l&1)*16 .. +16, applies the epilogue and
+// writes them with 16-byte stores. Everything indexed by the register array is unrolled, so the accumulators stay
+// in registers; the patch is then read with 16-byte LDS loads.
+constexpr int PATCH_STRIDE = 36;
+constexpr int PATCH_WORDS = 32 * PATCH_STRIDE;
 
-// Write one 32x32 block of results from a wave's LDS patch (row stride 33 words): lane l takes row l/2 and 16
-// consecutive columns, applies the epilogue and converts. Not inlined: the loop is over LDS, not registers.
-template <bool INT>
-__device__ __noinline__ void store_patch(const uint32_t* patch, void* C, int64_t ldc, int64_t row0, int64_t col0,
-                                         int64_t M, int64_t N, const Epilogue& e, int lane) {
-  const int r = lane >> 1, c0 = (lane & 1) * 16;
-  const int64_t m = row0 + r;
+template <bool INT, typename V>
+__device__ __forceinline__ void store_block(const V& block, uint32_t* patch, void* C, int64_t ldc, int64_t row0,
+                                            int64_t col0, int64_t M, int64_t N, const Epilogue& e, int lane) {
+  const int half = lane >> 5, r32 = lane & 31;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    if constexpr (INT)
+      patch[((r >> 2) * 8 + half * 4 + (r & 3)) * PATCH_STRIDE + r32] = (uint32_t)block[r];
+    else
+      patch[((r >> 2) * 8 + half * 4 + (r & 3)) * PATCH_STRIDE + r32] = __float_as_uint(block[r]);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the patch is written before any lane reads it
+  __builtin_amdgcn_wave_barrier();
+  const int rr = lane >> 1, c0 = (lane & 1) * 16;
+  uint32_t bits[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(patch + rr * PATCH_STRIDE + c0 + 4 * q);
+    bits[4 * q] = w[0], bits[4 * q + 1] = w[1], bits[4 * q + 2] = w[2], bits[4 * q + 3] = w[3];
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();  // the next block may overwrite the patch
+  const int64_t m = row0 + rr, n = col0 + c0;
   if (m >= M) return;
-  for (int c = c0; c < c0 + 16; ++c) {
-    const int64_t n = col0 + c;
-    if (n >= N) break;
-    const uint32_t bits = patch[r * 33 + c];
-    if (INT && e.out_kind == I32) {
-      static_cast<int32_t*>(C)[m * ldc + n] = (int32_t)bits;
-      continue;
+  const bool whole = n + 16 <= N && (ldc % 8) == 0 && (uintptr_t)C % 16 == 0;
+  if (INT && e.out_kind == I32) {
+    int32_t* out = static_cast<int32_t*>(C) + m * ldc + n;
+    if (whole && (ldc % 4) == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        reinterpret_cast<u32x4*>(out)[q] = u32x4{bits[4 * q], bits[4 * q + 1], bits[4 * q + 2], bits[4 * q + 3]};
+    } else {
+      for (int c = 0; c < 16 && n + c < N; ++c) out[c] = (int32_t)bits[c];
     }
-    const float v = apply_ops(INT ? (float)(int32_t)bits : __uint_as_float(bits), e, m, n);
-    switch (e.out_kind) {
-      case BF16: static_cast<uint16_t*>(C)[m * ldc + n] = f2bf(v); break;
-      case F16: static_cast<uint16_t*>(C)[m * ldc + n] = f2h(v); break;
-      default: static_cast<float*>(C)[m * ldc + n] = v; break;
+    return;
+  }
+  float v[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) v[c] = INT ? (float)(int32_t)bits[c] : __uint_as_float(bits[c]);
+  for (int i = 0; i < e.nops; ++i) {
+    const int op = e.op[i];
+    if (op % 3 == 0) {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], e.scalar[i]) : __fadd_rn(v[c], e.scalar[i]);
+    } else if (op % 3 == 1) {
+      const float s = e.vec[i][m];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], s) : __fadd_rn(v[c], s);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        const float s = n + c < N ? e.vec[i][n + c] : 0.0f;
+        v[c] = op < 3 ? __fmul_rn(v[c], s) : __fadd_rn(v[c], s);
+      }
     }
+  }
+  if (e.out_kind == F32) {
+    float* out = static_cast<float*>(C) + m * ldc + n;
+    if (whole) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        reinterpret_cast<f32x4*>(out)[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+    } else {
+      for (int c = 0; c < 16 && n + c < N; ++c) out[c] = v[c];
+    }
+    return;
+  }
+  uint32_t h[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    h[c] = e.out_kind == BF16 ? ((uint32_t)f2bf(v[2 * c]) | ((uint32_t)f2bf(v[2 * c + 1]) << 16))
+                              : ((uint32_t)f2h(v[2 * c]) | ((uint32_t)f2h(v[2 * c + 1]) << 16));
+  uint16_t* out = static_cast<uint16_t*>(C) + m * ldc + n;
+  if (whole) {
+    reinterpret_cast<u32x4*>(out)[0] = u32x4{h[0], h[1], h[2], h[3]};
+    reinterpret_cast<u32x4*>(out)[1] = u32x4{h[4], h[5], h[6], h[7]};
+  } else {
+    for (int c = 0; c < 16 && n + c < N; ++c) out[c] = (uint16_t)(h[c >> 1] >> ((c & 1) * 16));
   }
 }
 
@@ -142,6 +194,13 @@ __device__ __forceinline__ u32x4 load16(const uint8_t* __restrict__ p, int64_t b
     return u32x4{w[0], w[1], w[2], w[3]};
   }
 }
+
+// LDS swizzles. gfx950's LDS serves 16 lanes of a 16-byte read per cycle from 64 banks (256 bytes), so the 16
+// rows a read touches must land on 16 different 16-byte positions modulo 256 bytes. With 128-byte rows (8 chunks)
+// rows of equal parity share a window half, so chunk c of row r goes to slot c ^ ((r >> 1) & 7); with 64-byte rows
+// (4 chunks) rows of equal r & 3 share a quarter, so slot c ^ ((r >> 2) & 3).
+__device__ __forceinline__ int swz8(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int swz4(int row) { return (row >> 2) & 3; }
 
 // Tile index of this workgroup. Workgroups are dispatched round-robin over the 8 XCDs, so consecutive ids are
 // first regrouped per XCD (each XCD gets one contiguous range of tiles and its own L2 sees a compact panel), then
@@ -212,11 +271,11 @@ __global__ __launch_bounds__(256, 1) void gemm_tile(const uint8_t* __restrict__ 
   do {                                                                                                          \
     _Pragma("unroll") for (int p = 0; p < PA; ++p) {                                                            \
       const int row = lrow + 32 * p;                                                                            \
-      lds[s][row * 8 + (lchunk ^ (row & 7))] = ra[p];                                                           \
+      lds[s][row * 8 + (lchunk ^ swz8(row))] = ra[p];                                                           \
     }                                                                                                           \
     _Pragma("unroll") for (int p = 0; p < PB; ++p) {                                                            \
       const int row = BM + lrow + 32 * p;                                                                       \
-      lds[s][row * 8 + (lchunk ^ (row & 7))] = rb[p];                                                           \
+      lds[s][row * 8 + (lchunk ^ swz8(row))] = rb[p];                                                           \
     }                                                                                                           \
   } while (0)
 
@@ -236,7 +295,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile(const uint8_t* __restrict__ 
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
           const int chunk = (k * STEP + half * (STEP / 2)) / 16 + c;
-          fa[i][c] = lds[s][row * 8 + (chunk ^ (row & 7))];
+          fa[i][c] = lds[s][row * 8 + (chunk ^ swz8(row))];
         }
       }
 #pragma unroll
@@ -245,7 +304,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile(const uint8_t* __restrict__ 
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
           const int chunk = (k * STEP + half * (STEP / 2)) / 16 + c;
-          fb[j][c] = lds[s][row * 8 + (chunk ^ (row & 7))];
+          fb[j][c] = lds[s][row * 8 + (chunk ^ swz8(row))];
         }
       }
 #pragma unroll
@@ -261,21 +320,204 @@ __global__ __launch_bounds__(256, 1) void gemm_tile(const uint8_t* __restrict__ 
   // goes through a per-wave 32x33-word LDS patch so the global stores run along rows; only the register -> LDS
   // copy is unrolled, which keeps every accumulator index a compile-time constant (a runtime index would send the
   // whole accumulator array to scratch memory).
-  typedef std::remove_cv_t<std::remove_reference_t<decltype(acc[0][0][0])>> Elem;  // float or int
-  Elem* patch = reinterpret_cast<Elem*>(&lds[0][0]) + wave * (32 * 33);
+  uint32_t* patch = reinterpret_cast<uint32_t*>(&lds[0][0]) + wave * PATCH_WORDS;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+    for (int j = 0; j < TN; ++j)
+      store_block<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wm * (BM / WM) + i * 32,
+                                 n0 + wn * (BN / WN) + j * 32, M, N, e, lane);
+}
+
+// The pipelined main loop for whole tiles (M % BM == N % BN == 0, K a multiple of the BKB-byte slice, rows 16-byte
+// aligned). Operand slices go straight from global memory into LDS (global_load_lds_dwordx4, no register staging)
+// through a ring of STAGES buffers, so the loads of slice k + STAGES - 1 are in flight while slice k multiplies.
+// One barrier per slice publishes the landed slice and frees the oldest buffer; it is a bare s_barrier, because the
+// workgroup fence of __syncthreads() would wait for every outstanding load and drain the ring. A wave's load
+// instruction fills 1 KiB of LDS contiguously (lane i -> slot i), so each lane fetches the global chunk that belongs
+// at its swizzled slot. Fragments are double-buffered in registers: the LDS reads of step s + 1 (and, at the end of
+// a slice, of the next slice) are issued before the MFMAs of step s, and the scheduler is told to interleave one
+// LDS read or one global load with each MFMA, so the memory instructions issue in the shadow of the matrix core.
+template <int BKB>
+__device__ __forceinline__ int swzk(int row) {
+  return BKB == 128 ? swz8(row) : swz4(row);
+}
+
+template <int FMT, int BM, int BN, int WM, int WN, int STAGES, int BKB>
+__global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __restrict__ A,
+                                                             const uint8_t* __restrict__ B, void* __restrict__ C,
+                                                             int64_t M, int64_t N, int64_t kbytes, int64_t lda,
+                                                             int64_t ldb, int64_t ldc, Epilogue e) {
+  typedef Mfma<FMT> Unit;
+  typedef typename Unit::Acc Acc;
+  constexpr int THREADS = WM * WN * 64;
+  constexpr int CPR = BKB / 16;              // 16-byte chunks per row
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  constexpr int STEP = Unit::kBytes;         // bytes of K per MFMA
+  constexpr int CH = STEP / 32;              // 16-byte chunks per lane per MFMA operand
+  constexpr int KS = BKB / STEP;             // MFMA steps per slice
+  constexpr int ROWS_PER_LOAD = 1024 / BKB;  // rows one wave load instruction fills
+  constexpr int LOADS_A = BM / ROWS_PER_LOAD / (THREADS / 64), LOADS_B = BN / ROWS_PER_LOAD / (THREADS / 64);
+  constexpr int LOADS = LOADS_A + LOADS_B;   // load instructions per wave per slice
+  constexpr int STAGE_BYTES = (BM + BN) * BKB;
+  constexpr int VMCNT = (STAGES - 2) * LOADS;
+  static_assert(KS % 2 == 0, "an even number of MFMA steps per slice");
+  static_assert(LOADS_A * ROWS_PER_LOAD * (THREADS / 64) == BM && LOADS_B * ROWS_PER_LOAD * (THREADS / 64) == BN,
+                "the tile splits into whole wave loads");
+  static_assert(VMCNT <= 63, "vmcnt range");
+  static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS of one CU");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * STAGE_BYTES];
+
+  int tm, tn;
+  tile_of((int)(M / BM), (int)(N / BN), tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int half = lane >> 5, r32 = lane & 31;
+
+  // this lane's share of each wave load: its row within the 1 KiB block and the global chunk for its slot
+  const int lrow = lane / CPR, lslot = lane % CPR;
+  const uint8_t* a_src[LOADS_A];
+  const uint8_t* b_src[LOADS_B];
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        patch[((r >> 2) * 8 + half * 4 + (r & 3)) * 33 + r32] = acc[i][j][r];
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the patch is written before any lane reads it
-      __builtin_amdgcn_wave_barrier();
-      store_patch<FMT == FMT_I8>((const uint32_t*)patch, C, ldc, m0 + wm * (BM / WM) + i * 32, n0 + wn * (BN / WN) + j * 32, M, N,
-                                 e, lane);
-      __builtin_amdgcn_wave_barrier();
+  for (int j = 0; j < LOADS_A; ++j) {
+    const int row = (wave * LOADS_A + j) * ROWS_PER_LOAD + lrow;
+    a_src[j] = A + (m0 + row) * lda + (lslot ^ swzk<BKB>(row)) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < LOADS_B; ++j) {
+    const int row = (wave * LOADS_B + j) * ROWS_PER_LOAD + lrow;
+    b_src[j] = B + (n0 + row) * ldb + (lslot ^ swzk<BKB>(row)) * 16;
+  }
+  // fragment offsets (16-byte units within a stage) of every MFMA operand this lane reads
+  int a_off[TM][KS][CH], b_off[TN][KS][CH];
+#pragma unroll
+  for (int k = 0; k < KS; ++k)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int chunk = (k * STEP + half * (STEP / 2)) / 16 + c;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * (BM / WM) + i * 32 + r32;
+        a_off[i][k][c] = row * CPR + (chunk ^ swzk<BKB>(row));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = wn * (BN / WN) + j * 32 + r32;
+        b_off[j][k][c] = BM * CPR + row * CPR + (chunk ^ swzk<BKB>(row));
+      }
     }
+  const int nk = (int)(kbytes / BKB);
+
+#define KRN_ISSUE(slice)                                                                                        \
+  do {                                                                                                          \
+    uint8_t* stage = lds + ((slice) % STAGES) * STAGE_BYTES;                                                    \
+    const int64_t koff = (int64_t)(slice) * BKB;                                                                \
+    _Pragma("unroll") for (int j = 0; j < LOADS_A; ++j) __builtin_amdgcn_global_load_lds(                       \
+        (const void*)(a_src[j] + koff),                                                                         \
+        (__attribute__((address_space(3))) void*)(stage + (wave * LOADS_A + j) * 1024), 16, 0, 0);              \
+    _Pragma("unroll") for (int j = 0; j < LOADS_B; ++j) __builtin_amdgcn_global_load_lds(                       \
+        (const void*)(b_src[j] + koff),                                                                         \
+        (__attribute__((address_space(3))) void*)(stage + BM * BKB + (wave * LOADS_B + j) * 1024), 16, 0, 0);   \
+  } while (0)
+  // vmcnt(n) with lgkmcnt and expcnt left alone (gfx9 s_waitcnt encoding), then every LDS read of this wave done
+  // and the workgroup barrier
+#define KRN_PUBLISH(n)                                                                                          \
+  do {                                                                                                          \
+    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | ((n) & 15) | (((n) >> 4) << 14));                              \
+    __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00);                                                               \
+    __builtin_amdgcn_s_barrier();                                                                               \
+  } while (0)
+#define KRN_FRAGS(dst, slice, k)                                                                                \
+  do {                                                                                                          \
+    const u32x4* st = reinterpret_cast<const u32x4*>(lds + ((slice) % STAGES) * STAGE_BYTES);                   \
+    _Pragma("unroll") for (int i = 0; i < TM; ++i) _Pragma("unroll") for (int c = 0; c < CH; ++c)              \
+        dst##a[i][c] = st[a_off[i][k][c]];                                                                      \
+    _Pragma("unroll") for (int j = 0; j < TN; ++j) _Pragma("unroll") for (int c = 0; c < CH; ++c)              \
+        dst##b[j][c] = st[b_off[j][k][c]];                                                                      \
+  } while (0)
+#define KRN_MMA(src)                                                                                            \
+  _Pragma("unroll") for (int i = 0; i < TM; ++i) _Pragma("unroll") for (int j = 0; j < TN; ++j)                 \
+      Unit::step(acc[i][j], src##a[i], src##b[j])
+  // scheduling hints: one LDS read (0x100) or one global load (0x020) between consecutive MFMAs (0x008)
+#define KRN_WITH_READS()                                                                                        \
+  _Pragma("unroll") for (int q = 0; q < (TM + TN) * CH; ++q) {                                                  \
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                                          \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                          \
+  }
+#define KRN_WITH_LOADS()                                                                                        \
+  _Pragma("unroll") for (int q = 0; q < LOADS; ++q) {                                                           \
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                                          \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                                          \
+  }
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nk) KRN_ISSUE(s);
+  Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = Acc{};
+  u32x4 f0a[TM][CH], f0b[TN][CH], f1a[TM][CH], f1b[TN][CH];
+  if (nk > STAGES - 2) {
+    KRN_PUBLISH(VMCNT);
+  } else {
+    KRN_PUBLISH(0);
+  }
+  KRN_FRAGS(f0, 0, 0);
+  int kt = 0;
+  // steady state: every slice refills the ring (branch-free, so the scheduler can interleave)
+  for (; kt + STAGES - 1 < nk; ++kt) {
+#pragma unroll
+    for (int k = 0; k < KS; k += 2) {
+      KRN_FRAGS(f1, kt, k + 1);
+      if (k == 0) KRN_ISSUE(kt + STAGES - 1);
+      KRN_MMA(f0);
+      KRN_WITH_READS();
+      if (k == 0) KRN_WITH_LOADS();
+      if (k + 2 < KS) {
+        KRN_FRAGS(f0, kt, k + 2);
+      } else {
+        KRN_PUBLISH(VMCNT);
+        KRN_FRAGS(f0, kt + 1, 0);
+      }
+      KRN_MMA(f1);
+      KRN_WITH_READS();
+    }
+  }
+  // drain: the last STAGES - 1 slices are already in flight
+  for (; kt < nk; ++kt) {
+#pragma unroll
+    for (int k = 0; k < KS; k += 2) {
+      KRN_FRAGS(f1, kt, k + 1);
+      KRN_MMA(f0);
+      KRN_WITH_READS();
+      if (k + 2 < KS) {
+        KRN_FRAGS(f0, kt, k + 2);
+      } else if (kt + 1 < nk) {
+        KRN_PUBLISH(0);
+        KRN_FRAGS(f0, kt + 1, 0);
+      }
+      KRN_MMA(f1);
+      KRN_WITH_READS();
+    }
+  }
+#undef KRN_ISSUE
+#undef KRN_PUBLISH
+#undef KRN_FRAGS
+#undef KRN_MMA
+#undef KRN_WITH_READS
+#undef KRN_WITH_LOADS
+  __syncthreads();  // every wave is done with the ring before its LDS becomes the store patches
+
+  uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      store_block<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wm * (BM / WM) + i * 32,
+                                 n0 + wn * (BN / WN) + j * 32, M, N, e, lane);
 }
 
 }  // namespace krn
@@ -312,6 +554,35 @@ static int launch_gemm(const void* a, const void* b, void* c, int64_t m, int64_t
   return 0;
 }
 
+template <int FMT, int BM, int BN, int WM, int WN, int STAGES, int BKB>
+static int launch_pipe(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                       int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+  const int64_t tiles = (m / BM) * (n / BN);
+  if (tiles > 0x7fffffff) {
+    krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
+    return -1;
+  }
+  hipLaunchKernelGGL((gemm_pipe<FMT, BM, BN, WM, WN, STAGES, BKB>), dim3((unsigned)tiles), dim3(WM * WN * 64), 0, stream,
+                     (const uint8_t*)a, (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    krn_set_error("gemm launch: %s", hipGetErrorString(err));
+    return (int)err;
+  }
+  return 0;
+}
+
+// Whole 256 x 256 tiles: a ring of four 64-byte K slices (two MFMA steps each for bf16/f16/int8), or for fp8,
+// whose MFMA takes 64 bytes of K per step, two 128-byte slices.
+template <int FMT>
+static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                        int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+  if constexpr (FMT == FMT_FP8)
+    return launch_pipe<FMT, 256, 256, 2, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  else
+    return launch_pipe<FMT, 256, 256, 2, 2, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+}
+
 static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
                          int64_t elem, const Epilogue& e, hipStream_t stream) {
   const int64_t kbytes = k * elem, lda = k * elem, ldb = k * elem;
@@ -320,7 +591,9 @@ static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t
   const int64_t big = ((m + 255) / 256) * ((n + 255) / 256);
   const bool vec = kbytes % 16 == 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0;
   const bool large = big >= 256 && vec;
+  const bool whole = vec && m % 256 == 0 && n % 256 == 0 && kbytes % 128 == 0 && kbytes > 0 && large;
 #define KRN_GEMM(F)                                                                                    \
+  if (whole) return launch_whole<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                  \
   return large ? launch_gemm<F, 256, 256, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream)      \
                : launch_gemm<F, 128, 128, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream)
   switch (fmt) {
