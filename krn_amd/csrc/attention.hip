@@ -6,21 +6,36 @@
 // `o = (acc / total).to(dtype)`. Keys past the end of the sequence are invalid lanes: they take no part in the
 // maximum, the sum or the product.
 //
-// Layout (MI355X-first): a workgroup owns 128 query rows of one (batch, head); each of its 4 waves owns 32 rows and
+// Layout (MI355X-first). A workgroup owns 128 query rows of one (batch, head); each of its 4 waves owns 32 rows and
 // computes the transposed products S^T = K Q^T and O^T += V^T P^T with v_mfma_f32_32x32x16_{bf16,f16}. In that form
 // every lane holds one query row (lane & 31) and 16 of the keys of a 32-key block (its half-wave partner holds the
 // other 16), so the row maximum and sum are lane-local plus one exchange with lane ^ 32, the rescale of O is
-// lane-local, and P feeds the next MFMA straight from registers as its B operand. K and V^T tiles of 64 keys are
-// staged in LDS, double buffered; K rows are 16-byte-chunk swizzled by (key & 7) and V^T rows 8-byte-unit swizzled
-// by f(d) = (d ^ (d >> 3)) & 15, which keeps both the transposing writes and the fragment reads conflict-free.
+// lane-local, and P feeds the next MFMA straight from registers as its B operand. Q stays in registers for the
+// whole pass. K and V tiles of 64 keys stream through LDS in a two-slot ring filled by direct-to-LDS loads
+// (global_load_lds_dwordx4) while the previous tile multiplies; both keep the row-major [key][d] layout of global
+// memory. K is read as the A operand of S^T with 16-byte reads (chunk c of key row r at slot c ^ (r & 15)); V is
+// read as the A operand of O^T with ds_read_b64_tr_b16, which hands each lane four keys of one d column, so V never
+// needs a transposing copy (chunk c of key row r at slot c ^ 4 (r & 3)). Two workgroups share a CU, so each SIMD
+// interleaves the softmax of one wave with the MFMAs of another.
+//
+// Exact shortcuts, none of which changes a result bit: the row maximum of an unmasked tile is taken on the raw
+// scores and scaled once (rounding is monotonic, scale > 0); tiles wholly past a wave's last causal row are skipped
+// (their p are exp2(-1e30 - m) = 0 and their corr is 1); and when no row maximum of a wave moved, the rescale by
+// corr = exp2(0) = 1 is skipped.
 #include "common.h"
 
 namespace krn {
+
+typedef short v4s __attribute__((ext_vector_type(4)));
 
 template <bool BF>
 struct Half;
 template <>
 struct Half<true> {
+  __device__ static uint32_t pack(float lo, float hi) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, bf2{(__bf16)lo, (__bf16)hi});  // v_cvt_pk_bf16_f32, nearest even
+  }
   __device__ static uint16_t from(float x) { return f2bf(x); }
   __device__ static void mma(f32x16& c, u32x4 a, u32x4 b) {
     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
@@ -29,6 +44,7 @@ struct Half<true> {
 };
 template <>
 struct Half<false> {
+  __device__ static uint32_t pack(float lo, float hi) { return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16); }
   __device__ static uint16_t from(float x) { return f2h(x); }
   __device__ static void mma(f32x16& c, u32x4 a, u32x4 b) {
     c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
@@ -36,25 +52,37 @@ struct Half<false> {
   }
 };
 
-constexpr int BQ = 128;  // query rows per workgroup
+constexpr int BQ = 128;   // query rows per workgroup
 constexpr int BKEY = 64;  // keys per LDS tile
 
-__device__ __forceinline__ int vt_unit(int d, int unit) { return unit ^ ((d ^ (d >> 3)) & 15); }
+// LDS swizzles of the [key][d] tiles (64 banks serve 256 bytes per cycle). K: the 16-byte reads of 16 consecutive
+// keys must hit 16 distinct positions modulo 256 bytes. V: the transposed 8-byte reads cover 4 consecutive keys x
+// 64 bytes per 32 lanes. D = 128 (256-byte rows) and D = 64 (128-byte rows) need different XOR patterns.
+template <int D>
+__device__ __forceinline__ int k_slot(int key, int chunk) {
+  return D == 128 ? chunk ^ (key & 15) : chunk ^ ((key >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int v_slot(int key, int chunk) {
+  return D == 128 ? chunk ^ ((key & 3) << 2) : chunk ^ (((key >> 1) & 1) << 2);
+}
 
 template <bool BF, int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void attention_fwd(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+__global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                                                         const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
                                                         int64_t sq, int64_t sk, float scale, int q_tiles) {
   static_assert(D == 64 || D == 128, "head dimension 64 or 128");
-  constexpr int DCH = D / 8;                         // 16-byte chunks per K row
-  constexpr int KT_BYTES = BKEY * D * 2;             // one K tile
-  constexpr int VT_BYTES = D * BKEY * 2;             // one V^T tile
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][KT_BYTES + VT_BYTES];
+  constexpr int DCH = D / 8;                // 16-byte chunks per key row
+  constexpr int TILE_BYTES = BKEY * D * 2;  // one K (or V) tile
+  constexpr int ROWS_PER_LOAD = 1024 / (D * 2);
+  constexpr int LOADS = BKEY / ROWS_PER_LOAD / 4;  // wave load instructions per tile, per operand
+  static_assert(LOADS * ROWS_PER_LOAD * 4 == BKEY, "whole wave loads");
+  static_assert(DCH <= 16, "swizzle range");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][2 * TILE_BYTES];
 
   // Heavy (late) query tiles first, so the causal tail is spread over the machine.
-  const int tile_linear = blockIdx.x;
-  const int head = tile_linear / q_tiles;
-  const int qt = CAUSAL ? (q_tiles - 1 - tile_linear % q_tiles) : tile_linear % q_tiles;
+  const int head = blockIdx.x / q_tiles;
+  const int qt = CAUSAL ? (q_tiles - 1 - (int)(blockIdx.x % q_tiles)) : (int)(blockIdx.x % q_tiles);
   const int64_t q0 = (int64_t)qt * BQ;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, half = lane >> 5, r32 = lane & 31;
   const uint16_t* q = Q + (int64_t)head * sq * D;
@@ -62,7 +90,7 @@ __global__ __launch_bounds__(256, 1) void attention_fwd(const uint16_t* __restri
   const uint16_t* v = V + (int64_t)head * sk * D;
   uint16_t* o = O + (int64_t)head * sq * D;
 
-  // This lane's query row and its Q fragments (B operand of S^T = K Q^T): 8 contiguous d per MFMA step.
+  // this lane's query row and its Q fragments (B operand of S^T = K Q^T): 8 contiguous d per MFMA step
   const int64_t qrow = q0 + wave * 32 + r32;
   u32x4 qf[D / 16];
 #pragma unroll
@@ -74,100 +102,92 @@ __global__ __launch_bounds__(256, 1) void attention_fwd(const uint16_t* __restri
   for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
   float m = -1.0e30f, total = 0.0f;
 
-  // key range of this workgroup and of this wave
-  int64_t kend = sk;
-  if (CAUSAL) kend = min(sk, q0 + BQ);
-  const int64_t wave_last_q = q0 + wave * 32 + 31;
+  const int64_t kend = CAUSAL ? min(sk, q0 + BQ) : sk;
+  const int64_t wave_first_q = q0 + wave * 32, wave_last_q = wave_first_q + 31;
   const int ntiles = (int)((kend + BKEY - 1) / BKEY);
 
-  // staging: K tile = 64 rows x DCH chunks; V tile = 16 groups of 4 keys x DCH chunks (4 rows per thread)
-  constexpr int KLOADS = BKEY * DCH / 256;           // 16-byte K chunks per thread
-  constexpr int VGROUPS = BKEY / 4 * DCH;            // (4-key, 8-d) blocks per tile
-  constexpr int VLOADS = (VGROUPS + 255) / 256;      // blocks per thread (the last round may be partial)
-  static_assert(KLOADS >= 1 && BKEY * DCH % 256 == 0, "K tile splits evenly over the workgroup");
-  u32x4 kr[KLOADS], vr[VLOADS][4];
-
-#define KRN_FA_LOAD(tile)                                                                                      \
-  do {                                                                                                         \
-    const int64_t c0 = (int64_t)(tile) * BKEY;                                                                 \
-    _Pragma("unroll") for (int i = 0; i < KLOADS; ++i) {                                                       \
-      const int id = t + 256 * i, key = id / DCH, ch = id % DCH;                                               \
-      kr[i] = c0 + key < sk ? *reinterpret_cast<const u32x4*>(k + (c0 + key) * D + ch * 8) : u32x4{};          \
-    }                                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < VLOADS; ++i) {                                                       \
-      const int id = t + 256 * i, group = id / DCH, ch = id % DCH;                                             \
-      _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                          \
-        const int64_t key = c0 + group * 4 + r;                                                                \
-        vr[i][r] = (id < VGROUPS && key < sk) ? *reinterpret_cast<const u32x4*>(v + key * D + ch * 8) : u32x4{}; \
-      }                                                                                                        \
-    }                                                                                                          \
+  // direct-to-LDS loads: lane -> (row within its 1 KiB block, slot); rows past the sequence read the last row
+  // (finite data whose scores are masked to -inf, so their p is 0)
+  const int lrow = lane / DCH, lslot = lane % DCH;
+#define KRN_FA_ISSUE(tile)                                                                                    \
+  do {                                                                                                        \
+    uint8_t* st = &lds[(tile) & 1][0];                                                                        \
+    _Pragma("unroll") for (int j = 0; j < LOADS; ++j) {                                                       \
+      const int row = (wave * LOADS + j) * ROWS_PER_LOAD + lrow;                                              \
+      const int64_t key = min((int64_t)(tile) * BKEY + row, sk - 1);                                          \
+      __builtin_amdgcn_global_load_lds((const void*)(k + key * D + k_slot<D>(row, lslot) * 8),                    \
+                                       (__attribute__((address_space(3))) void*)(st + (wave * LOADS + j) * 1024), \
+                                       16, 0, 0);                                                             \
+      __builtin_amdgcn_global_load_lds(                                                                       \
+          (const void*)(v + key * D + v_slot<D>(row, lslot) * 8),                                                \
+          (__attribute__((address_space(3))) void*)(st + TILE_BYTES + (wave * LOADS + j) * 1024), 16, 0, 0);  \
+    }                                                                                                         \
+  } while (0)
+#define KRN_FA_PUBLISH()                                                                                      \
+  do {                                                                                                        \
+    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00);  /* vmcnt(0) */                                             \
+    __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00); /* lgkmcnt(0) */                                            \
+    __builtin_amdgcn_s_barrier();                                                                             \
   } while (0)
 
-#define KRN_FA_STORE(buf)                                                                                      \
-  do {                                                                                                         \
-    u32x4* kl = reinterpret_cast<u32x4*>(&lds[buf][0]);                                                        \
-    _Pragma("unroll") for (int i = 0; i < KLOADS; ++i) {                                                       \
-      const int id = t + 256 * i, key = id / DCH, ch = id % DCH;                                               \
-      kl[key * DCH + (ch ^ (key & 7))] = kr[i];                                                                \
-    }                                                                                                          \
-    uint2* vl = reinterpret_cast<uint2*>(&lds[buf][KT_BYTES]);                                                 \
-    _Pragma("unroll") for (int i = 0; i < VLOADS; ++i) {                                                       \
-      const int id = t + 256 * i, group = id / DCH, ch = id % DCH;                                             \
-      if (id < VGROUPS) _Pragma("unroll") for (int e = 0; e < 8; ++e) {                                       \
-        const int d = ch * 8 + e;                                                                              \
-        const uint32_t w = e >> 1, sh = (e & 1) * 16;                                                          \
-        uint32_t k0 = (vr[i][0][w] >> sh) & 0xffffu, k1 = (vr[i][1][w] >> sh) & 0xffffu;                       \
-        uint32_t k2 = (vr[i][2][w] >> sh) & 0xffffu, k3 = (vr[i][3][w] >> sh) & 0xffffu;                       \
-        vl[d * (BKEY / 4) + vt_unit(d, group)] = uint2{k0 | (k1 << 16), k2 | (k3 << 16)};                      \
-      }                                                                                                        \
-    }                                                                                                          \
-  } while (0)
+  if (ntiles > 0) KRN_FA_ISSUE(0);
+  KRN_FA_PUBLISH();
 
-  if (ntiles > 0) {
-    KRN_FA_LOAD(0);
-    KRN_FA_STORE(0);
-  }
-  __syncthreads();
+  // V^T fragment address pieces for ds_read_b64_tr_b16: lane group g = lane / 16 reads keys
+  // K0 + (lane % 16) / 4 at d columns dblk * 32 + (g % 2) * 16 + 4 * (lane % 4)
+  const int g = lane >> 4, a16 = lane & 15;
+  const int tr_key = (g >> 1) * 4 + (a16 >> 2);
+  const int tr_col = (g & 1) * 16 + 4 * (a16 & 3);
 
   for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
     const int64_t c0 = (int64_t)tile * BKEY;
-    if (tile + 1 < ntiles) KRN_FA_LOAD(tile + 1);
-
+    if (tile + 1 < ntiles) KRN_FA_ISSUE(tile + 1);
     const bool active = !CAUSAL || c0 <= wave_last_q;
     if (active) {
-      const u32x4* kl = reinterpret_cast<const u32x4*>(&lds[buf][0]);
-      const uint2* vl = reinterpret_cast<const uint2*>(&lds[buf][KT_BYTES]);
+      const uint8_t* st = &lds[tile & 1][0];
+      const u32x4* kl = reinterpret_cast<const u32x4*>(st);
       // S^T for the two 32-key halves of the tile
-      f32x16 st[2];
+      f32x16 s[2];
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb) {
-        st[hb] = f32x16{};
+        s[hb] = f32x16{};
         const int key = hb * 32 + r32;
 #pragma unroll
-        for (int s = 0; s < D / 16; ++s) {
-          const int ch = s * 2 + half;
-          Half<BF>::mma(st[hb], kl[key * DCH + (ch ^ (key & 7))], qf[s]);
-        }
+        for (int j = 0; j < D / 16; ++j) Half<BF>::mma(s[hb], kl[key * DCH + k_slot<D>(key, j * 2 + half)], qf[j]);
       }
-      // scale, mask, running maximum (lane-local over 32 values, then with the partner lane)
-      float tmax = -INFINITY;
+      const bool masked = c0 + BKEY > sk || (CAUSAL && c0 + BKEY - 1 > wave_first_q) || !(scale > 0.0f);
+      float m_new;
+      if (!masked) {
+        float raw = s[0][0];
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb)
+        for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t key = c0 + hb * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-          float x = st[hb][r] * scale;
-          if (CAUSAL && key > qrow) x = -1.0e30f;
-          if (key >= sk) x = -INFINITY;  // an invalid lane: no part in the max, the sum or the product
-          st[hb][r] = x;
-          tmax = fmaxf(tmax, x);
-        }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float m_new = fmaxf(m, tmax);
-      const float corr = exp2f(m - m_new);
+          for (int r = 0; r < 16; ++r) raw = fmaxf(raw, s[hb][r]);
+        raw = fmaxf(raw, __shfl_xor(raw, 32));
+        m_new = fmaxf(m, raw * scale);
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[hb][r] = s[hb][r] * scale;
+      } else {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t key = c0 + hb * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+            float x = s[hb][r] * scale;
+            if (CAUSAL && key > qrow) x = -1.0e30f;
+            if (key >= sk) x = -INFINITY;  // an invalid lane: no part in the max, the sum or the product
+            s[hb][r] = x;
+            tmax = fmaxf(tmax, x);
+          }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        m_new = fmaxf(m, tmax);
+      }
+      // p = exp2(s - m_new) in f32 for the sum, packed to 16 bits as P^T, the B operand: [half block][k16 step]
       float psum = 0.0f;
-      u32x4 pf[2][2];  // P^T as the B operand: [half block][k16 step], 8 keys per lane
+      u32x4 pf[2][2];
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
@@ -175,53 +195,61 @@ __global__ __launch_bounds__(256, 1) void attention_fwd(const uint16_t* __restri
           uint32_t w[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float p0 = exp2f(st[hb][step * 8 + 2 * j] - m_new);
-            const float p1 = exp2f(st[hb][step * 8 + 2 * j + 1] - m_new);
-            psum += p0 + p1;
-            w[j] = (uint32_t)Half<BF>::from(p0) | ((uint32_t)Half<BF>::from(p1) << 16);
+            const float p0 = __builtin_amdgcn_exp2f(s[hb][step * 8 + 2 * j] - m_new);
+            const float p1 = __builtin_amdgcn_exp2f(s[hb][step * 8 + 2 * j + 1] - m_new);
+            psum += p0;
+            psum += p1;
+            w[j] = Half<BF>::pack(p0, p1);
           }
           pf[hb][step] = u32x4{w[0], w[1], w[2], w[3]};
         }
       psum += __shfl_xor(psum, 32);
-      total = total * corr + psum;
+      if (__builtin_amdgcn_ballot_w64(m_new != m) != 0) {  // some row maximum moved: rescale by exp2(m - m_new)
+        const float corr = __builtin_amdgcn_exp2f(m - m_new);
+        total = total * corr;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
+      }
+      total = total + psum;
       m = m_new;
-#pragma unroll
-      for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
-      // O^T += V^T P^T: A operand lane = d row, the same 8 keys per lane as P (two 4-key units)
+      // O^T += V^T P^T: A operand lane = d row, the same 8 keys per lane as P (two 4-key transposed reads)
 #pragma unroll
       for (int i = 0; i < D / 32; ++i) {
-        const int d = i * 32 + r32;
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
           for (int step = 0; step < 2; ++step) {
-            const int u0 = hb * 8 + step * 4 + half, u1 = u0 + 2;
-            const uint2 lo = vl[d * (BKEY / 4) + vt_unit(d, u0)];
-            const uint2 hi = vl[d * (BKEY / 4) + vt_unit(d, u1)];
-            Half<BF>::mma(acc[i], u32x4{lo.x, lo.y, hi.x, hi.y}, pf[hb][step]);
+            u32x4 va;
+#pragma unroll
+            for (int part = 0; part < 2; ++part) {
+              const int key = hb * 32 + step * 16 + part * 8 + tr_key;
+              const int col = i * 32 + tr_col;  // 4 consecutive d: half a 16-byte chunk
+              const int off = key * (D * 2) + v_slot<D>(key, col >> 3) * 16 + (col & 7) * 2;
+              const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (__attribute__((address_space(3))) v4s*)(st + TILE_BYTES + off));
+              const u32x2 w = __builtin_bit_cast(u32x2, x);
+              va[part * 2] = w[0];
+              va[part * 2 + 1] = w[1];
+            }
+            Half<BF>::mma(acc[i], va, pf[hb][step]);
           }
       }
     }
-    if (tile + 1 < ntiles) KRN_FA_STORE(buf ^ 1);
-    __syncthreads();
+    KRN_FA_PUBLISH();
   }
-#undef KRN_FA_LOAD
-#undef KRN_FA_STORE
+#undef KRN_FA_ISSUE
+#undef KRN_FA_PUBLISH
 
   if (qrow < sq) {
-    const float inv_total = 1.0f;  // acc / total is a division per element, as the tile program writes it
-    (void)inv_total;
 #pragma unroll
     for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = i * 32 + g * 8 + half * 4;
-        uint32_t lo = (uint32_t)Half<BF>::from(acc[i][g * 4 + 0] / total) |
-                      ((uint32_t)Half<BF>::from(acc[i][g * 4 + 1] / total) << 16);
-        uint32_t hi = (uint32_t)Half<BF>::from(acc[i][g * 4 + 2] / total) |
-                      ((uint32_t)Half<BF>::from(acc[i][g * 4 + 3] / total) << 16);
+      for (int gq = 0; gq < 4; ++gq) {
+        const int d = i * 32 + gq * 8 + half * 4;
+        const uint32_t lo = Half<BF>::pack(acc[i][gq * 4 + 0] / total, acc[i][gq * 4 + 1] / total);
+        const uint32_t hi = Half<BF>::pack(acc[i][gq * 4 + 2] / total, acc[i][gq * 4 + 3] / total);
         *reinterpret_cast<uint2*>(o + qrow * D + d) = uint2{lo, hi};
       }
   }
@@ -262,6 +290,11 @@ extern "C" int krn_attention_fwd(int kind, const void* q, const void* k, const v
   if (blocks == 0) return 0;
   if (blocks > 0x7fffffff) {
     krn_set_error("attention: %lld workgroups exceed the grid limit", (long long)blocks);
+    return -1;
+  }
+  if (sk == 0) {
+    // no keys: the tile program divides 0 by 0
+    krn_set_error("attention: an empty key sequence has no softmax");
     return -1;
   }
   hipStream_t s = (hipStream_t)stream;

@@ -266,7 +266,7 @@ class Launch:
         sk = k.shape[1]
         if d != plan.d or k.shape != (bh, sk, d) or v.shape != (bh, sk, d) or o.shape != (bh, sq, d):
             return False
-        if (grid.x, grid.y, grid.z) != (-(-sq // plan.bq), bh, 1):
+        if (grid.x, grid.y, grid.z) != (-(-sq // plan.bq), bh, 1) or sk == 0:
             return False
         library.attention_fwd(plan.dtype, q.pointer, k.pointer, v.pointer, o.pointer, bh, sq, sk, d,
                               float(np.float32(params[plan.scale])), plan.causal, stream.handle)
