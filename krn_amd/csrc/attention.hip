@@ -18,10 +18,11 @@
 // needs a transposing copy (chunk c of key row r at slot c ^ 4 (r & 3)). Two workgroups share a CU, so each SIMD
 // interleaves the softmax of one wave with the MFMAs of another.
 //
-// Exact shortcuts, none of which changes a result bit: the row maximum of an unmasked tile is taken on the raw
-// scores and scaled once (rounding is monotonic, scale > 0); tiles wholly past a wave's last causal row are skipped
-// (their p are exp2(-1e30 - m) = 0 and their corr is 1); and when no row maximum of a wave moved, the rescale by
-// corr = exp2(0) = 1 is skipped.
+// Shortcuts. Exact: the row maximum of an unmasked tile is taken on the raw scores and scaled once (rounding is
+// monotonic, scale > 0); tiles wholly past a wave's last causal row are skipped (their p are exp2(-1e30 - m) = 0 and
+// their corr is 1). Equal up to rounding: the exponent argument s * scale - m is one fused multiply-add on unmasked
+// tiles, and the running maximum used as the exponent base is refreshed only when it is beaten by more than 8
+// (p <= 2^8), which scales p, acc and total by the same power of two and leaves acc / total unchanged.
 #include "common.h"
 
 namespace krn {
@@ -149,45 +150,57 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
       // S^T for the two 32-key halves of the tile
       f32x16 s[2];
 #pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
-        s[hb] = f32x16{};
-        const int key = hb * 32 + r32;
+      for (int hb = 0; hb < 2; ++hb) s[hb] = f32x16{};
+      // the two halves interleaved, so consecutive MFMAs never wait for each other's result
 #pragma unroll
-        for (int j = 0; j < D / 16; ++j) Half<BF>::mma(s[hb], kl[key * DCH + k_slot<D>(key, j * 2 + half)], qf[j]);
-      }
+      for (int j = 0; j < D / 16; ++j)
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          const int key = hb * 32 + r32;
+          Half<BF>::mma(s[hb], kl[key * DCH + k_slot<D>(key, j * 2 + half)], qf[j]);
+        }
       const bool masked = c0 + BKEY > sk || (CAUSAL && c0 + BKEY - 1 > wave_first_q) || !(scale > 0.0f);
-      float m_new;
+      float tmax;
       if (!masked) {
         float raw = s[0][0];
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) raw = fmaxf(raw, s[hb][r]);
-        raw = fmaxf(raw, __shfl_xor(raw, 32));
-        m_new = fmaxf(m, raw * scale);
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[hb][r] = s[hb][r] * scale;
+        tmax = raw * scale;
       } else {
-        float tmax = -INFINITY;
+        tmax = -INFINITY;
+        const int key0 = (int)c0 + half * 4, row = (int)qrow, valid = (int)(sk - c0);
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int64_t key = c0 + hb * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+            const int key = key0 + hb * 32 + (r >> 2) * 8 + (r & 3);
             float x = s[hb][r] * scale;
-            if (CAUSAL && key > qrow) x = -1.0e30f;
-            if (key >= sk) x = -INFINITY;  // an invalid lane: no part in the max, the sum or the product
+            if (CAUSAL && key > row) x = -1.0e30f;
+            if (key - (int)c0 >= valid) x = -INFINITY;  // an invalid lane: no part in the max, sum or product
             s[hb][r] = x;
             tmax = fmaxf(tmax, x);
           }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        m_new = fmaxf(m, tmax);
       }
-      // p = exp2(s - m_new) in f32 for the sum, packed to 16 bits as P^T, the B operand: [half block][k16 step]
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      // Lazy rescale: the exponent base m only moves when some row maximum of the wave exceeds it by more than
+      // 8 (so every p <= 2^8); acc and total are then rescaled by exp2(m - m_new). Keeping a stale base scales p,
+      // acc and total alike, which leaves acc / total unchanged up to rounding.
+      if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
+        const float m_new = fmaxf(m, tmax);
+        const float corr = __builtin_amdgcn_exp2f(m - m_new);
+        total = total * corr;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
+        m = m_new;
+      }
+      // p = exp2(s - m) in f32 for the sum, packed to 16 bits as P^T, the B operand: [half block][k16 step]
       float psum = 0.0f;
       u32x4 pf[2][2];
+      const float neg_m = -m;
 #pragma unroll
       for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
@@ -195,8 +208,9 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
           uint32_t w[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float p0 = __builtin_amdgcn_exp2f(s[hb][step * 8 + 2 * j] - m_new);
-            const float p1 = __builtin_amdgcn_exp2f(s[hb][step * 8 + 2 * j + 1] - m_new);
+            const float x0 = s[hb][step * 8 + 2 * j], x1 = s[hb][step * 8 + 2 * j + 1];
+            const float p0 = __builtin_amdgcn_exp2f(masked ? x0 + neg_m : __builtin_fmaf(x0, scale, neg_m));
+            const float p1 = __builtin_amdgcn_exp2f(masked ? x1 + neg_m : __builtin_fmaf(x1, scale, neg_m));
             psum += p0;
             psum += p1;
             w[j] = Half<BF>::pack(p0, p1);
@@ -204,23 +218,15 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
           pf[hb][step] = u32x4{w[0], w[1], w[2], w[3]};
         }
       psum += __shfl_xor(psum, 32);
-      if (__builtin_amdgcn_ballot_w64(m_new != m) != 0) {  // some row maximum moved: rescale by exp2(m - m_new)
-        const float corr = __builtin_amdgcn_exp2f(m - m_new);
-        total = total * corr;
-#pragma unroll
-        for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
-      }
       total = total + psum;
-      m = m_new;
       // O^T += V^T P^T: A operand lane = d row, the same 8 keys per lane as P (two 4-key transposed reads)
+      // (the D / 32 accumulators innermost, so consecutive MFMAs are independent)
 #pragma unroll
-      for (int i = 0; i < D / 32; ++i) {
+      for (int hb = 0; hb < 2; ++hb) {
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
+        for (int step = 0; step < 2; ++step)
 #pragma unroll
-          for (int step = 0; step < 2; ++step) {
+          for (int i = 0; i < D / 32; ++i) {
             u32x4 va;
 #pragma unroll
             for (int part = 0; part < 2; ++part) {
