@@ -76,6 +76,24 @@ def attention_bf16(device, steps, warmup, rng, batch=4, heads=32, seq=4096, d=12
     return ms, 2.0 * batch * heads * seq * seq * d  # causal: half of 4 B H S^2 D
 
 
+def transpose_copy(device, steps, warmup, rng, n=8192):
+    """The calibration kernel for HBM byte counters: an n x n 16-bit transpose reads and writes 2 n^2 bytes each."""
+    from krn_amd import T
+    from krn_amd.runtime import library
+
+    src = device.to_device(rng.integers(0, 1 << 16, (n, n), dtype=np.uint16), T.bf16)
+    dst = device.empty(T.bf16, n, n)
+    stream = device.default_stream
+
+    def run():
+        library.transpose16(src.pointer, dst.pointer, n, n, stream.handle)
+
+    for _ in range(warmup):
+        run()
+    ms = events_ms(stream, run, steps)
+    return ms, 2 * n * n
+
+
 def quantize_e4m3(x: np.ndarray) -> tuple[np.ndarray, np.float32]:
     from krn_amd.formats import e4m3_encode
 
@@ -153,7 +171,8 @@ def main() -> None:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    parser.add_argument("--only", default="", help="comma list of extra legs to run (fa, fp8, int8)")
+    parser.add_argument("--only", default="", help="comma list of extra legs to run (fa, fp8, int8, copy); "
+                        "copy is the known-size calibration kernel for HBM byte counters and runs only when named")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the tile kernels shard by output "
@@ -191,6 +210,11 @@ def main() -> None:
                 "ms": round(i_ms, 4), "tops": round(i_ops / i_ms / 1e9, 1),
                 "frac_of_int8_peak": round(i_ops / i_ms / 1e9 / PEAK["int8"], 4),
                 "gbps": round(i_bytes / i_ms / 1e6, 1), "frac_of_hbm": round(i_bytes / i_ms / 1e6 / HBM_PEAK, 4)}
+    if "copy" in legs:
+        print("[bench] 16-bit transpose 8192^2 (counter calibration)", file=sys.stderr, flush=True)
+        c_ms, c_bytes = transpose_copy(device, args.steps, args.warmup, rng)
+        extra["transpose16_8192x8192"] = {"ms": round(c_ms, 4), "bytes_read": c_bytes, "bytes_written": c_bytes,
+                                          "gbps": round(2 * c_bytes / c_ms / 1e6, 1)}
     baseline = None
     if not args.no_cpu:
         print("[bench] CPU baseline (oracle C backend, bounded sample)", file=sys.stderr, flush=True)
