@@ -520,6 +520,86 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
                                  n0 + wn * (BN / WN) + j * 32, M, N, e, lane);
 }
 
+// Skinny products (M <= 128), the HBM-bound shapes: B (N x K) is streamed once and A is small enough to be served
+// from L2. A workgroup owns 32 output columns and all M rows (MT blocks of 32); its WAVES waves split K, wave w
+// taking the 128-byte K slices w, w + WAVES, ..., so that together they read WAVES * 128 contiguous bytes of each
+// row per round. Operands go straight from global memory into MFMA registers with no LDS staging: lane (r32, half)
+// loads bytes [half * 64, half * 64 + 64) of its row's slice as four 16-byte loads, and MFMA step s takes the s-th
+// 16 bytes of them (32 bytes for fp8). A and B use the same K permutation, so the dot products are unchanged. The
+// partial sums meet in LDS, and waves 0..MT-1 each store one 32 x 32 block through the common epilogue.
+template <int FMT, int MT, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __restrict__ A,
+                                                              const uint8_t* __restrict__ B, void* __restrict__ C,
+                                                              int64_t M, int64_t N, int64_t kbytes, int64_t lda,
+                                                              int64_t ldb, int64_t ldc, Epilogue e) {
+  typedef Mfma<FMT> Unit;
+  typedef typename Unit::Acc Acc;
+  typedef std::conditional_t<FMT == FMT_I8, int, float> Elem;
+  constexpr int CH = Unit::kBytes / 32;  // 16-byte registers per lane per MFMA step
+  constexpr int STEPS = 4 / CH;          // MFMA steps per 128-byte slice
+  constexpr int RED_WORDS = WAVES * MT * 16 * 64;
+  constexpr int LDS_WORDS = RED_WORDS > WAVES * PATCH_WORDS ? RED_WORDS : WAVES * PATCH_WORDS;
+  __shared__ __attribute__((aligned(16))) uint32_t lds[LDS_WORDS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, r32 = lane & 31;
+  const int64_t n0 = (int64_t)blockIdx.x * 32;
+  // columns past the end read the last one; the epilogue does not store them
+  const uint8_t* bp = B + min(n0 + r32, N - 1) * ldb + half * 64;
+  const uint8_t* ap[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) ap[t] = A + min((int64_t)t * 32 + r32, M - 1) * lda + half * 64;
+  const int nk = (int)(kbytes / 128);
+  Acc acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = Acc{};
+  for (int first = wave; first < nk; first += WAVES * U) {
+    u32x4 rb[U][4], ra[U][MT][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int slice = first + u * WAVES;
+      if (slice < nk) {
+        const int64_t off = (int64_t)slice * 128;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) rb[u][q] = *reinterpret_cast<const u32x4*>(bp + off + q * 16);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if (t * 32 + r32 < M) {  // rows past the end need no load: their results are never stored
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ra[u][t][q] = *reinterpret_cast<const u32x4*>(ap[t] + off + q * 16);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ra[u][t][q] = u32x4{};
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (first + u * WAVES < nk) {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) Unit::step(acc[t], &ra[u][t][s * CH], &rb[u][s * CH]);
+      }
+    }
+  }
+  Elem* partial = reinterpret_cast<Elem*>(lds);
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) partial[((wave * MT + t) * 16 + r) * 64 + lane] = acc[t][r];
+  __syncthreads();
+  Acc sum = Acc{};
+  if (wave < MT) {
+    for (int v = 0; v < WAVES; ++v)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sum[r] += partial[((v * MT + wave) * 16 + r) * 64 + lane];
+  }
+  __syncthreads();
+  if (wave < MT)
+    store_block<FMT == FMT_I8>(sum, lds + wave * PATCH_WORDS, C, ldc, (int64_t)wave * 32, n0, M, N, e, lane);
+}
+
 }  // namespace krn
 
 using namespace krn;
@@ -572,6 +652,34 @@ static int launch_pipe(const void* a, const void* b, void* c, int64_t m, int64_t
   return 0;
 }
 
+template <int FMT, int MT>
+static int launch_skinny_mt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                            int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+  constexpr int WAVES = 8, U = MT <= 2 ? 4 : 2;
+  hipLaunchKernelGGL((gemm_skinny<FMT, MT, WAVES, U>), dim3((unsigned)((n + 31) / 32)), dim3(WAVES * 64), 0, stream,
+                     (const uint8_t*)a, (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    krn_set_error("gemm launch: %s", hipGetErrorString(err));
+    return (int)err;
+  }
+  return 0;
+}
+
+// M <= 128 rows with 16-byte aligned rows of a multiple of 128 bytes: one workgroup per 32 output columns.
+template <int FMT>
+static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+  switch ((m + 31) / 32) {
+    case 1: return launch_skinny_mt<FMT, 1>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    case 2: return launch_skinny_mt<FMT, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    case 3: return launch_skinny_mt<FMT, 3>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    case 4: return launch_skinny_mt<FMT, 4>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  }
+  krn_set_error("gemm: %lld rows are too many for the skinny kernel", (long long)m);
+  return -1;
+}
+
 // Whole 256 x 256 tiles: a ring of four 64-byte K slices (two MFMA steps each for bf16/f16/int8), or for fp8,
 // whose MFMA takes 64 bytes of K per step, two 128-byte slices.
 template <int FMT>
@@ -592,8 +700,11 @@ static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t
   const bool vec = kbytes % 16 == 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0;
   const bool large = big >= 256 && vec;
   const bool whole = vec && m % 256 == 0 && n % 256 == 0 && kbytes % 128 == 0 && kbytes > 0 && large;
+  // few rows: stream B once with every CU busy (whole tiles would leave most CUs idle)
+  const bool skinny = vec && m > 0 && m <= 128 && n > 0 && kbytes % 128 == 0 && kbytes > 0;
 #define KRN_GEMM(F)                                                                                    \
   if (whole) return launch_whole<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                  \
+  if (skinny) return launch_skinny<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                \
   return large ? launch_gemm<F, 256, 256, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream)      \
                : launch_gemm<F, 128, 128, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream)
   switch (fmt) {

@@ -14,7 +14,7 @@ from tests.kernels import tile_programs as programs
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(50, 38, 72), (257, 129, 40), (512, 512, 512), (300, 1000, 136), (50, 38, 70), (16, 8, 8), (130, 257, 33),
-          (1, 384, 256), (16, 8, 0)]
+          (1, 384, 256), (16, 8, 0), (40, 300, 128), (70, 96, 384), (97, 33, 64)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
