@@ -11,18 +11,20 @@
 // every lane holds one query row (lane & 31) and 16 of the keys of a 32-key block (its half-wave partner holds the
 // other 16), so the row maximum and sum are lane-local plus one exchange with lane ^ 32, the rescale of O is
 // lane-local, and P feeds the next MFMA straight from registers as its B operand. Q stays in registers for the
-// whole pass. K and V tiles of 64 keys stream through LDS in a two-slot ring filled by direct-to-LDS loads
-// (global_load_lds_dwordx4) while the previous tile multiplies; both keep the row-major [key][d] layout of global
-// memory. K is read as the A operand of S^T with 16-byte reads (chunk c of key row r at slot c ^ (r & 15)); V is
-// read as the A operand of O^T with ds_read_b64_tr_b16, which hands each lane four keys of one d column, so V never
-// needs a transposing copy (chunk c of key row r at slot c ^ 4 (r & 3)). Two workgroups share a CU, so each SIMD
-// interleaves the softmax of one wave with the MFMAs of another.
+// whole pass. K and V tiles of 64 keys stream through LDS (a ring of three K tiles and two V tiles) filled by
+// direct-to-LDS loads (global_load_lds_dwordx4); both keep the row-major [key][d] layout of global memory. K is read
+// as the A operand of S^T with 16-byte reads (chunk c of key row r at slot c ^ (r & 15)); V is read as the A
+// operand of O^T with ds_read_b64_tr_b16, which hands each lane four keys of one d column, so V never needs a
+// transposing copy (chunk c of key row r at slot c ^ 4 (r & 3)). The key loop is software-pipelined in 32-key
+// halves: the score MFMAs of half h + 1 are issued before the exp2 / sum / pack of half h, so the matrix core and
+// the vector ALU of one wave work at the same time. Two workgroups share a CU, so each SIMD also interleaves two
+// waves. Causal launches run the late (long) query tiles of every head first.
 //
-// Shortcuts. Exact: the row maximum of an unmasked tile is taken on the raw scores and scaled once (rounding is
-// monotonic, scale > 0); tiles wholly past a wave's last causal row are skipped (their p are exp2(-1e30 - m) = 0 and
-// their corr is 1). Equal up to rounding: the exponent argument s * scale - m is one fused multiply-add on unmasked
-// tiles, and the running maximum used as the exponent base is refreshed only when it is beaten by more than 8
-// (p <= 2^8), which scales p, acc and total by the same power of two and leaves acc / total unchanged.
+// Shortcuts. Exact: the row maximum of an unmasked half is taken on the raw scores and scaled once (rounding is
+// monotonic, scale > 0); halves wholly past a wave's last causal row are skipped (their p are exp2(-1e30 - m) = 0
+// and their corr is 1). Equal up to rounding: the exponent argument s * scale - m is one fused multiply-add on
+// unmasked halves, and the running maximum used as the exponent base is refreshed only when it is beaten by more
+// than 8 (p <= 2^8), which scales p, acc and total by the same power of two and leaves acc / total unchanged.
 #include "common.h"
 
 namespace krn {
@@ -68,10 +70,13 @@ __device__ __forceinline__ int v_slot(int key, int chunk) {
   return D == 128 ? chunk ^ ((key & 3) << 2) : chunk ^ (((key >> 1) & 1) << 2);
 }
 
-template <bool BF, int D, bool CAUSAL>
+// `causal` is a run-time argument rather than a template parameter: both variants then get the same code and
+// register allocation, and a non-causal launch only sees its limits at +infinity.
+template <bool BF, int D>
 __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                                                         const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
-                                                        int64_t sq, int64_t sk, float scale, int q_tiles) {
+                                                        int64_t sq, int64_t sk, float scale, int q_tiles,
+                                                        int causal) {
   static_assert(D == 64 || D == 128, "head dimension 64 or 128");
   constexpr int DCH = D / 8;                // 16-byte chunks per key row
   constexpr int TILE_BYTES = BKEY * D * 2;  // one K (or V) tile
@@ -79,11 +84,12 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
   constexpr int LOADS = BKEY / ROWS_PER_LOAD / 4;  // wave load instructions per tile, per operand
   static_assert(LOADS * ROWS_PER_LOAD * 4 == BKEY, "whole wave loads");
   static_assert(DCH <= 16, "swizzle range");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][2 * TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * TILE_BYTES];
 
-  // Heavy (late) query tiles first, so the causal tail is spread over the machine.
-  const int head = blockIdx.x / q_tiles;
-  const int qt = CAUSAL ? (q_tiles - 1 - (int)(blockIdx.x % q_tiles)) : (int)(blockIdx.x % q_tiles);
+  // Causal: the heavy (late) query tiles of every head first, so the short ones fill the tail of the launch.
+  const int heads = (int)(gridDim.x / q_tiles);
+  const int head = causal ? (int)(blockIdx.x % heads) : (int)(blockIdx.x / q_tiles);
+  const int qt = causal ? (q_tiles - 1 - (int)(blockIdx.x / heads)) : (int)(blockIdx.x % q_tiles);
   const int64_t q0 = (int64_t)qt * BQ;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, half = lane >> 5, r32 = lane & 31;
   const uint16_t* q = Q + (int64_t)head * sq * D;
@@ -103,25 +109,46 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
   for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
   float m = -1.0e30f, total = 0.0f;
 
-  const int64_t kend = CAUSAL ? min(sk, q0 + BQ) : sk;
-  const int64_t wave_first_q = q0 + wave * 32, wave_last_q = wave_first_q + 31;
+  const int64_t kend = causal ? min(sk, q0 + BQ) : sk;
+  // the causal limits of this wave's rows (no limit without a causal mask)
+  const int64_t NONE = (int64_t)1 << 62;
+  const int64_t wave_first_q = causal ? q0 + wave * 32 : NONE, wave_last_q = causal ? q0 + wave * 32 + 31 : NONE;
+  const int row_limit = causal ? (int)qrow : 0x7fffffff;  // keys beyond it are masked
   const int ntiles = (int)((kend + BKEY - 1) / BKEY);
+  const int nhalves = (int)((kend + 31) / 32);
 
-  // direct-to-LDS loads: lane -> (row within its 1 KiB block, slot); rows past the sequence read the last row
-  // (finite data whose scores are masked to -inf, so their p is 0)
+  // LDS: a ring of three K tiles, then two V tiles. The loop is software-pipelined in 32-key halves: while half h
+  // turns its scores into P (VALU), the scores of half h + 1 multiply (MFMA); then O += V P for half h runs beside
+  // the row maximum of half h + 1. So the K tile of the next half is read before this tile's V: tile iteration t
+  // reads K(t) and K(t + 1), and V(t). It loads K(t + 2) into the slot K(t - 1) left and V(t + 1) into the slot
+  // V(t - 1) left; one barrier per tile publishes both.
+  // Direct-to-LDS loads: lane -> (row within its 1 KiB block, slot).
+  // Each lane's element offsets inside a tile are fixed: computed once here; a load adds the tile's base (uniform)
   const int lrow = lane / DCH, lslot = lane % DCH;
-#define KRN_FA_ISSUE(tile)                                                                                    \
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  int koff[LOADS], voff[LOADS];
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    const int row = (wave * LOADS + j) * ROWS_PER_LOAD + lrow;
+    koff[j] = row * D + k_slot<D>(row, lslot) * 8;
+    voff[j] = row * D + v_slot<D>(row, lslot) * 8;
+  }
+#define KRN_FA_LOAD(src, tile, base, OFF)                                                                     \
   do {                                                                                                        \
-    uint8_t* st = &lds[(tile) & 1][0];                                                                        \
-    _Pragma("unroll") for (int j = 0; j < LOADS; ++j) {                                                       \
-      const int row = (wave * LOADS + j) * ROWS_PER_LOAD + lrow;                                              \
-      const int64_t key = min((int64_t)(tile) * BKEY + row, sk - 1);                                          \
-      __builtin_amdgcn_global_load_lds((const void*)(k + key * D + k_slot<D>(row, lslot) * 8),                    \
-                                       (__attribute__((address_space(3))) void*)(st + (wave * LOADS + j) * 1024), \
-                                       16, 0, 0);                                                             \
-      __builtin_amdgcn_global_load_lds(                                                                       \
-          (const void*)(v + key * D + v_slot<D>(row, lslot) * 8),                                                \
-          (__attribute__((address_space(3))) void*)(st + TILE_BYTES + (wave * LOADS + j) * 1024), 16, 0, 0);  \
+    const int64_t t0 = (int64_t)(tile) * BKEY;                                                                \
+    if (t0 + BKEY <= sk) {                                                                                    \
+      const uint16_t* tb = (src) + t0 * D;                                                                    \
+      _Pragma("unroll") for (int j = 0; j < LOADS; ++j) __builtin_amdgcn_global_load_lds(                     \
+          (const void*)(tb + OFF[j]),                                                                         \
+          (__attribute__((address_space(3))) void*)(lds + (base) + (wave_s * LOADS + j) * 1024), 16, 0, 0);   \
+    } else { /* the ragged last tile: rows past the sequence read the last row (masked, so their p is 0) */   \
+      _Pragma("unroll") for (int j = 0; j < LOADS; ++j) {                                                     \
+        const int row = (wave * LOADS + j) * ROWS_PER_LOAD + lrow;                                            \
+        const int64_t key = min(t0 + row, sk - 1);                                                            \
+        __builtin_amdgcn_global_load_lds(                                                                     \
+            (const void*)((src) + key * D + (OFF[j] - row * D)),                                              \
+            (__attribute__((address_space(3))) void*)(lds + (base) + (wave_s * LOADS + j) * 1024), 16, 0, 0); \
+      }                                                                                                       \
     }                                                                                                         \
   } while (0)
 #define KRN_FA_PUBLISH()                                                                                      \
@@ -130,123 +157,148 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
     __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00); /* lgkmcnt(0) */                                            \
     __builtin_amdgcn_s_barrier();                                                                             \
   } while (0)
-
-  if (ntiles > 0) KRN_FA_ISSUE(0);
-  KRN_FA_PUBLISH();
+  // S^T of the 32-key half `hb` of the K tile at LDS offset `kb`
+#define KRN_FA_SCORES(S, kb, hb)                                                                              \
+  do {                                                                                                        \
+    const u32x4* kl = reinterpret_cast<const u32x4*>(lds + (kb));                                            \
+    const int key = (hb) * 32 + r32;                                                                          \
+    S = f32x16{};                                                                                             \
+    _Pragma("unroll") for (int j = 0; j < D / 16; ++j) Half<BF>::mma(S, kl[key * DCH + k_slot<D>(key, j * 2 + half)], qf[j]); \
+  } while (0)
+  // the scaled row maximum of an unmasked half, from the raw scores (rounding is monotonic and scale > 0)
+#define KRN_FA_RAWMAX(S, out)                                                                                 \
+  do {                                                                                                        \
+    float raw = S[0];                                                                                         \
+    _Pragma("unroll") for (int r = 1; r < 16; ++r) raw = fmaxf(raw, S[r]);                                    \
+    raw *= scale;                                                                                             \
+    out = fmaxf(raw, __shfl_xor(raw, 32));                                                                    \
+  } while (0)
+  // p = exp2(s * sc - m) in f32 for the row sum, packed to 16 bits as P^T, the B operand of two k16 steps
+#define KRN_FA_EXP(S, sc)                                                                                     \
+  do {                                                                                                        \
+    const float neg_m = -m;                                                                                   \
+    _Pragma("unroll") for (int step = 0; step < 2; ++step) {                                                  \
+      uint32_t w[4];                                                                                          \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                         \
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(S[step * 8 + 2 * j], sc, neg_m));              \
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(S[step * 8 + 2 * j + 1], sc, neg_m));          \
+        psum[step] += p0 + p1;                                                                                \
+        w[j] = Half<BF>::pack(p0, p1);                                                                        \
+      }                                                                                                       \
+      pf[step] = u32x4{w[0], w[1], w[2], w[3]};                                                               \
+    }                                                                                                         \
+  } while (0)
+  // O^T += V^T P^T for the keys of half `hb` of the V tile at `vb`: A operand lane = d row, the same 8 keys per
+  // lane as P (two 4-key transposed reads); the D / 32 accumulators innermost, so consecutive MFMAs are independent
+#define KRN_FA_PV(vb, hb)                                                                                     \
+  do {                                                                                                        \
+    _Pragma("unroll") for (int step = 0; step < 2; ++step) _Pragma("unroll") for (int i = 0; i < D / 32; ++i) { \
+      u32x4 va;                                                                                               \
+      _Pragma("unroll") for (int part = 0; part < 2; ++part) {                                                \
+        const int key = (hb) * 32 + step * 16 + part * 8 + tr_key;                                            \
+        const int col = i * 32 + tr_col;                                                                      \
+        const int off = key * (D * 2) + v_slot<D>(key, col >> 3) * 16 + (col & 7) * 2;                       \
+        const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(                                                \
+            (__attribute__((address_space(3))) v4s*)(lds + (vb) + off));                                      \
+        const u32x2 w = __builtin_bit_cast(u32x2, x);                                                         \
+        va[part * 2] = w[0];                                                                                  \
+        va[part * 2 + 1] = w[1];                                                                              \
+      }                                                                                                       \
+      Half<BF>::mma(acc[i], va, pf[step]);                                                                    \
+    }                                                                                                         \
+  } while (0)
 
   // V^T fragment address pieces for ds_read_b64_tr_b16: lane group g = lane / 16 reads keys
   // K0 + (lane % 16) / 4 at d columns dblk * 32 + (g % 2) * 16 + 4 * (lane % 4)
   const int g = lane >> 4, a16 = lane & 15;
   const int tr_key = (g >> 1) * 4 + (a16 >> 2);
   const int tr_col = (g & 1) * 16 + 4 * (a16 & 3);
+  const bool positive = scale > 0.0f;
+  constexpr int V_BASE = 3 * TILE_BYTES;
 
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int64_t c0 = (int64_t)tile * BKEY;
-    if (tile + 1 < ntiles) KRN_FA_ISSUE(tile + 1);
-    const bool active = !CAUSAL || c0 <= wave_last_q;
-    if (active) {
-      const uint8_t* st = &lds[tile & 1][0];
-      const u32x4* kl = reinterpret_cast<const u32x4*>(st);
-      // S^T for the two 32-key halves of the tile
-      f32x16 s[2];
-#pragma unroll
-      for (int hb = 0; hb < 2; ++hb) s[hb] = f32x16{};
-      // the two halves interleaved, so consecutive MFMAs never wait for each other's result
-#pragma unroll
-      for (int j = 0; j < D / 16; ++j)
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-          const int key = hb * 32 + r32;
-          Half<BF>::mma(s[hb], kl[key * DCH + k_slot<D>(key, j * 2 + half)], qf[j]);
-        }
-      const bool masked = c0 + BKEY > sk || (CAUSAL && c0 + BKEY - 1 > wave_first_q) || !(scale > 0.0f);
-      float tmax;
-      if (!masked) {
-        float raw = s[0][0];
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) raw = fmaxf(raw, s[hb][r]);
-        tmax = raw * scale;
-      } else {
-        tmax = -INFINITY;
-        const int key0 = (int)c0 + half * 4, row = (int)qrow, valid = (int)(sk - c0);
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = key0 + hb * 32 + (r >> 2) * 8 + (r & 3);
-            float x = s[hb][r] * scale;
-            if (CAUSAL && key > row) x = -1.0e30f;
-            if (key - (int)c0 >= valid) x = -INFINITY;  // an invalid lane: no part in the max, sum or product
-            s[hb][r] = x;
-            tmax = fmaxf(tmax, x);
-          }
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      // Lazy rescale: the exponent base m only moves when some row maximum of the wave exceeds it by more than
-      // 8 (so every p <= 2^8); acc and total are then rescaled by exp2(m - m_new). Keeping a stale base scales p,
-      // acc and total alike, which leaves acc / total unchanged up to rounding.
-      if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {
-        const float m_new = fmaxf(m, tmax);
-        const float corr = __builtin_amdgcn_exp2f(m - m_new);
-        total = total * corr;
-#pragma unroll
-        for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
-        m = m_new;
-      }
-      // p = exp2(s - m) in f32 for the sum, packed to 16 bits as P^T, the B operand: [half block][k16 step]
-      float psum = 0.0f;
-      u32x4 pf[2][2];
-      const float neg_m = -m;
-#pragma unroll
-      for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-        for (int step = 0; step < 2; ++step) {
-          uint32_t w[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float x0 = s[hb][step * 8 + 2 * j], x1 = s[hb][step * 8 + 2 * j + 1];
-            const float p0 = __builtin_amdgcn_exp2f(masked ? x0 + neg_m : __builtin_fmaf(x0, scale, neg_m));
-            const float p1 = __builtin_amdgcn_exp2f(masked ? x1 + neg_m : __builtin_fmaf(x1, scale, neg_m));
-            psum += p0;
-            psum += p1;
-            w[j] = Half<BF>::pack(p0, p1);
-          }
-          pf[hb][step] = u32x4{w[0], w[1], w[2], w[3]};
-        }
-      psum += __shfl_xor(psum, 32);
-      total = total + psum;
-      // O^T += V^T P^T: A operand lane = d row, the same 8 keys per lane as P (two 4-key transposed reads)
-      // (the D / 32 accumulators innermost, so consecutive MFMAs are independent)
-#pragma unroll
-      for (int hb = 0; hb < 2; ++hb) {
-#pragma unroll
-        for (int step = 0; step < 2; ++step)
-#pragma unroll
-          for (int i = 0; i < D / 32; ++i) {
-            u32x4 va;
-#pragma unroll
-            for (int part = 0; part < 2; ++part) {
-              const int key = hb * 32 + step * 16 + part * 8 + tr_key;
-              const int col = i * 32 + tr_col;  // 4 consecutive d: half a 16-byte chunk
-              const int off = key * (D * 2) + v_slot<D>(key, col >> 3) * 16 + (col & 7) * 2;
-              const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (__attribute__((address_space(3))) v4s*)(st + TILE_BYTES + off));
-              const u32x2 w = __builtin_bit_cast(u32x2, x);
-              va[part * 2] = w[0];
-              va[part * 2 + 1] = w[1];
-            }
-            Half<BF>::mma(acc[i], va, pf[hb][step]);
-          }
-      }
-    }
+  f32x16 sa, sb;
+  float tmax_next = -INFINITY;  // the scaled row maximum of the next half's raw scores
+  if (ntiles > 0) {
+    KRN_FA_LOAD(k, 0, 0, koff);
+    KRN_FA_LOAD(v, 0, V_BASE, voff);
+    if (ntiles > 1) KRN_FA_LOAD(k, 1, TILE_BYTES, koff);
     KRN_FA_PUBLISH();
+    KRN_FA_SCORES(sa, 0, 0);  // the first half is active for every wave
+    KRN_FA_RAWMAX(sa, tmax_next);
   }
-#undef KRN_FA_ISSUE
+
+  // One pipeline step over half `hb` of tile `t` (K slot `kcur`, the next tile's K slot `knext`): SC holds its
+  // scores, SN receives those of the following half.
+#define KRN_FA_HALF(t, hb, SC, SN, kcur, knext)                                                               \
+  do {                                                                                                        \
+    const int h = 2 * (t) + (hb);                                                                             \
+    const int64_t c0 = (int64_t)h * 32;                                                                       \
+    const bool active = h < nhalves && c0 <= wave_last_q;                                                                                             \
+    const bool next = h + 1 < nhalves && c0 + 32 <= wave_last_q;                                                                               \
+    if (active) {                                                                                             \
+      const bool masked = c0 + 32 > sk || c0 + 31 > wave_first_q || !positive;                                                  \
+      float tmax = tmax_next;                                                                                 \
+      if (masked) {                                                                                           \
+        float mx = -INFINITY;                                                                                 \
+        const int key0 = (int)c0 + half * 4, valid = (int)(sk - c0);                                                                   \
+        _Pragma("unroll") for (int r = 0; r < 16; ++r) {                                                      \
+          const int key = key0 + (r >> 2) * 8 + (r & 3);                                                      \
+          float x = SC[r] * scale;                                                                            \
+          if (key > row_limit) x = -1.0e30f;                                                                  \
+          if (key - (int)c0 >= valid) x = -INFINITY; /* an invalid lane: no part in max, sum or product */    \
+          SC[r] = x;                                                                                          \
+          mx = fmaxf(mx, x);                                                                                  \
+        }                                                                                                     \
+        tmax = fmaxf(mx, __shfl_xor(mx, 32));                                                                 \
+      }                                                                                                       \
+      /* Lazy rescale: the exponent base m only moves when some row maximum of the wave exceeds it by more    \
+         than 8 (so every p <= 2^8); acc and total are then rescaled by exp2(m - m_new). A stale base scales  \
+         p, acc and total alike, which leaves acc / total unchanged up to rounding. */                        \
+      if (__builtin_amdgcn_ballot_w64(tmax > m + 8.0f) != 0) {                                                \
+        const float m_new = fmaxf(m, tmax);                                                                   \
+        const float corr = __builtin_amdgcn_exp2f(m - m_new);                                                 \
+        total = total * corr;                                                                                 \
+        _Pragma("unroll") for (int i = 0; i < D / 32; ++i) _Pragma("unroll") for (int r = 0; r < 16; ++r)     \
+            acc[i][r] *= corr;                                                                                \
+        m = m_new;                                                                                            \
+      }                                                                                                       \
+      /* masked halves already hold scaled scores: one fused multiply-add serves both (x * 1 - m is exact) */ \
+      const float sc = masked ? 1.0f : scale;                                                                 \
+      float psum[2] = {0.0f, 0.0f};                                                                           \
+      u32x4 pf[2];                                                                                            \
+      if (next) {                                                                                             \
+        if ((hb) == 0) KRN_FA_SCORES(SN, kcur, 1);                                                            \
+        else KRN_FA_SCORES(SN, knext, 0);                                                                     \
+        KRN_FA_EXP(SC, sc);                                                                                   \
+        KRN_FA_PV(V_BASE + ((t) & 1) * TILE_BYTES, hb);                                                       \
+        KRN_FA_RAWMAX(SN, tmax_next);                                                                         \
+      } else {                                                                                                \
+        KRN_FA_EXP(SC, sc);                                                                                   \
+        KRN_FA_PV(V_BASE + ((t) & 1) * TILE_BYTES, hb);                                                       \
+      }                                                                                                       \
+      const float ps = psum[0] + psum[1];                                                                     \
+      total = total + (ps + __shfl_xor(ps, 32));                                                              \
+    }                                                                                                         \
+  } while (0)
+
+  int kcur = 0;  // LDS offset of K(t); K(t + 1) and K(t + 2) follow around the ring
+  for (int t = 0; t < ntiles; ++t) {
+    const int knext = kcur == 2 * TILE_BYTES ? 0 : kcur + TILE_BYTES;
+    const int kfree = knext == 2 * TILE_BYTES ? 0 : knext + TILE_BYTES;
+    if (t + 2 < ntiles) KRN_FA_LOAD(k, t + 2, kfree, koff);
+    if (t + 1 < ntiles) KRN_FA_LOAD(v, t + 1, V_BASE + ((t + 1) & 1) * TILE_BYTES, voff);
+    KRN_FA_HALF(t, 0, sa, sb, kcur, knext);
+    KRN_FA_HALF(t, 1, sb, sa, kcur, knext);
+    KRN_FA_PUBLISH();
+    kcur = knext;
+  }
+#undef KRN_FA_LOAD
 #undef KRN_FA_PUBLISH
+#undef KRN_FA_SCORES
+#undef KRN_FA_RAWMAX
+#undef KRN_FA_EXP
+#undef KRN_FA_PV
+#undef KRN_FA_HALF
 
   if (qrow < sq) {
 #pragma unroll
@@ -265,13 +317,13 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
 
 using namespace krn;
 
-template <bool BF, int D, bool CAUSAL>
+template <bool BF, int D>
 static void launch_attention(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t sq,
-                             int64_t sk, float scale, hipStream_t stream) {
+                             int64_t sk, float scale, int causal, hipStream_t stream) {
   const int q_tiles = (int)((sq + BQ - 1) / BQ);
   dim3 grid((unsigned)(bh * q_tiles)), block(256);
-  hipLaunchKernelGGL((attention_fwd<BF, D, CAUSAL>), grid, block, 0, stream, (const uint16_t*)q, (const uint16_t*)k,
-                     (const uint16_t*)v, (uint16_t*)o, sq, sk, scale, q_tiles);
+  hipLaunchKernelGGL((attention_fwd<BF, D>), grid, block, 0, stream, (const uint16_t*)q, (const uint16_t*)k,
+                     (const uint16_t*)v, (uint16_t*)o, sq, sk, scale, q_tiles, causal);
 }
 
 extern "C" int krn_attention_fwd(int kind, const void* q, const void* k, const void* v, void* o, int64_t bh,
@@ -305,9 +357,8 @@ extern "C" int krn_attention_fwd(int kind, const void* q, const void* k, const v
   }
   hipStream_t s = (hipStream_t)stream;
   const bool bf = kind == BF16;
-#define KRN_FA(BFV, DV)                                                       \
-  (causal ? launch_attention<BFV, DV, true>(q, k, v, o, bh, sq, sk, scale, s) \
-          : launch_attention<BFV, DV, false>(q, k, v, o, bh, sq, sk, scale, s))
+#define KRN_FA(BFV, DV) \
+  launch_attention<BFV, DV>(q, k, v, o, bh, sq, sk, scale, causal != 0, s)
   if (bf && d == 128) KRN_FA(true, 128);
   else if (bf) KRN_FA(true, 64);
   else if (d == 128) KRN_FA(false, 128);
