@@ -94,6 +94,26 @@ def transpose_copy(device, steps, warmup, rng, n=8192):
     return ms, 2 * n * n
 
 
+def vendor_gemm_bf16(steps, warmup, n=8192):
+    """The same bf16 product through torch.matmul (hipBLASLt): a reference point for the headline, never the
+    product (krn_amd itself does not use torch)."""
+    import torch
+
+    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    for _ in range(warmup):
+        c = a @ b.T
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        c = a @ b.T
+    end.record()
+    torch.cuda.synchronize()
+    del c
+    return start.elapsed_time(end) / steps
+
+
 def quantize_e4m3(x: np.ndarray) -> tuple[np.ndarray, np.float32]:
     from krn_amd.formats import e4m3_encode
 
@@ -171,8 +191,9 @@ def main() -> None:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    parser.add_argument("--only", default="", help="comma list of extra legs to run (fa, fp8, int8, copy); "
-                        "copy is the known-size calibration kernel for HBM byte counters and runs only when named")
+    parser.add_argument("--only", default="", help="comma list of extra legs to run (fa, fp8, int8, copy, "
+                        "blas); copy (the known-size calibration kernel for HBM byte counters) and blas (the same bf16 "
+                        "product through torch/hipBLASLt, a vendor reference point) run only when named")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the tile kernels shard by output "
@@ -215,6 +236,10 @@ def main() -> None:
         c_ms, c_bytes = transpose_copy(device, args.steps, args.warmup, rng)
         extra["transpose16_8192x8192"] = {"ms": round(c_ms, 4), "bytes_read": c_bytes, "bytes_written": c_bytes,
                                           "gbps": round(2 * c_bytes / c_ms / 1e6, 1)}
+    if "blas" in legs:
+        print("[bench] hipBLASLt bf16 gemm 8192^3 (torch.matmul, reference point)", file=sys.stderr, flush=True)
+        v_ms = vendor_gemm_bf16(args.steps, args.warmup)
+        extra["hipblaslt_bf16_gemm_8192_reference"] = {"ms": round(v_ms, 4), "tflops": round(flops / v_ms / 1e9, 1)}
     baseline = None
     if not args.no_cpu:
         print("[bench] CPU baseline (oracle C backend, bounded sample)", file=sys.stderr, flush=True)

@@ -680,15 +680,16 @@ static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64
   return -1;
 }
 
-// Whole 256 x 256 tiles: a ring of four 64-byte K slices (two MFMA steps each for bf16/f16/int8), or for fp8,
-// whose MFMA takes 64 bytes of K per step, two 128-byte slices.
+// Whole 256 x 256 tiles: for bf16/f16 a ring of four 64-byte K slices (two MFMA steps each); for fp8 and int8 two
+// 128-byte slices (two fp8 or four int8 MFMA steps each).
 template <int FMT>
 static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  if constexpr (FMT == FMT_FP8)
-    return launch_pipe<FMT, 256, 256, 2, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  // eight waves (4 x 2, each 64 x 128 of the tile): two waves per SIMD hide each other's LDS and barrier waits
+  if constexpr (FMT == FMT_FP8 || FMT == FMT_I8)
+    return launch_pipe<FMT, 256, 256, 4, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   else
-    return launch_pipe<FMT, 256, 256, 2, 2, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    return launch_pipe<FMT, 256, 256, 4, 2, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
 }
 
 static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
