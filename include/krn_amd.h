@@ -25,9 +25,13 @@ extern "C" {
 enum krn_kind { KRN_F32 = 0, KRN_F16 = 1, KRN_BF16 = 2, KRN_F8E4M3 = 3, KRN_I8 = 4, KRN_I32 = 5 };
 
 /* Epilogue operations of krn_gemm_nt, applied in order to the float32 accumulator, each rounded to float32:
- * x * s, x * row[m], x * col[n], x + s, x + row[m], x + col[n]. */
+ * x * s, x * row[m], x * col[n], x + s, x + row[m], x + col[n], and the activations of krn's lib.matmul epilogues
+ * (reference src/krn/lib/lib_kernels.py:31-48 with the formulas of src/krn/compiler/emit.py:112-114):
+ * relu x < 0 ? 0 : x, gelu 0.5 x (1 + erf(x / sqrt 2)), silu x / (1 + exp(-x)). A row or column vector is float32
+ * unless its operation code adds KRN_VEC_F16 or KRN_VEC_BF16. */
 enum krn_epilogue_op {
-  KRN_MUL_SCALAR = 0, KRN_MUL_ROW = 1, KRN_MUL_COL = 2, KRN_ADD_SCALAR = 3, KRN_ADD_ROW = 4, KRN_ADD_COL = 5
+  KRN_MUL_SCALAR = 0, KRN_MUL_ROW = 1, KRN_MUL_COL = 2, KRN_ADD_SCALAR = 3, KRN_ADD_ROW = 4, KRN_ADD_COL = 5,
+  KRN_RELU = 6, KRN_GELU = 7, KRN_SILU = 8, KRN_VEC_F16 = 16, KRN_VEC_BF16 = 32
 };
 
 /* C[m, n] = epilogue(sum_k A[m, k] * B[n, k]), A: M x K, B: N x K, C: M x N, all row-major.
@@ -39,9 +43,10 @@ enum krn_epilogue_op {
  * reference, src/krn/compiler/matrix.py:129-139) or KRN_I8 (int32 accumulation; refused by the reference capture,
  * src/krn/compiler/capture.py:3193-3201). out_kind: KRN_F32, KRN_F16, KRN_BF16 (round to nearest even), or KRN_I32
  * (int8 operands and no epilogue operations only). ops/scalars/vectors: nops <= 4 epilogue operations; vectors[i]
- * is a device float array of length M (row) or N (column), unused for scalar operations. */
+ * is a device array of length M (row) or N (column), unused for scalar operations and activations. The activations
+ * and the bias vector serve krn's lib.matmul kernel (reference src/krn/lib/lib_ours.py:58-75). */
 int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n, int64_t k,
-                int nops, const int* ops, const float* scalars, const float* const* vectors, void* stream);
+                int nops, const int* ops, const float* scalars, const void* const* vectors, void* stream);
 
 /* out (cols x rows) = in (rows x cols) transposed, 16-bit elements: turns the B operand of `a[rows, ks] @ b[ks, cols]`
  * (reference examples/04_libraries/01_gemm_tiles.py:34-40) K-contiguous for krn_gemm_nt. */

@@ -65,7 +65,8 @@ TENSOR_RANKS = {"Matrix": 2, "Vector": 1, "Tensor3": 3}
 ARITHMETIC = {"add": Op.ADD, "sub": Op.SUB, "mul": Op.MUL, "div": Op.DIV, "truediv": Op.DIV}
 UNARY_MATH = {
     "exp": Fn.EXP, "exp2": Fn.EXP2, "log": Fn.LOG, "log2": Fn.LOG2, "sqrt": Fn.SQRT, "rsqrt": Fn.RSQRT,
-    "abs": Fn.ABS, "tanh": Fn.TANH, "relu": Fn.RELU,
+    "abs": Fn.ABS, "tanh": Fn.TANH, "relu": Fn.RELU, "gelu": Fn.GELU, "silu": Fn.SILU, "sigmoid": Fn.SIGMOID,
+    "erf": Fn.ERF,
 }  # fmt: skip
 BINARY_MATH = {"maximum": Fn.MAXIMUM, "minimum": Fn.MINIMUM}
 BINOPS = {ast.Add: Op.ADD, ast.Sub: Op.SUB, ast.Mult: Op.MUL, ast.Div: Op.DIV, ast.Mod: Op.MOD}
@@ -629,8 +630,18 @@ class Capture:
         kind = TileType(dtype, shape) if shape else dtype
         return Select(kind, condition, x, y, line=node.lineno)
 
+    def tensor_dtype(self, node: ast.AST) -> Dtype | None:
+        """The element type of `x.dtype` for a tensor parameter `x`, else None."""
+        if isinstance(node, ast.Attribute) and node.attr == "dtype" and isinstance(node.value, ast.Name):
+            for name, kind in self.params:
+                if name == node.value.id and isinstance(kind, TensorType):
+                    return kind.dtype
+        return None
+
     def method(self, name: str, base: Expr, node: ast.Call) -> Expr:
         if name == "to":
+            if len(node.args) == 1 and (element := self.tensor_dtype(node.args[0])) is not None:
+                return self.cast(base, element)
             if len(node.args) != 1 or (dtype := dtype_name(node.args[0])) is None:
                 raise self.error(node, "`.to(dtype)` takes one element type")
             return self.cast(base, D.BY_NAME[dtype])
@@ -684,11 +695,11 @@ class Capture:
         return value.value
 
     def broadcast(self, a: tuple[int, ...], b: tuple[int, ...], node: ast.AST) -> tuple[int, ...]:
-        """numpy broadcasting of tile shapes, aligned from the right."""
+        """numpy broadcasting of tile shapes, aligned from the right (reference compiler/capture.py:1531-1541)."""
         if not a or not b:
             return a or b
-        if len(a) != len(b):
-            raise self.error(node, f"tile shapes {list(a)} and {list(b)} have different ranks")
+        width = max(len(a), len(b))
+        a, b = (1,) * (width - len(a)) + a, (1,) * (width - len(b)) + b
         out = []
         for x, y in zip(a, b):
             if x != y and 1 not in (x, y):

@@ -4,10 +4,11 @@ kernels serve, and lower everything else through the generic HIP emitter.
 What `lower` returns is a plan the HIP backend launches:
 
 * `GemmPlan`: `acc = zeros(...)`, one K loop of `acc += a[rows, ks] @ b[cols, ks].transpose()` (or `b[ks, cols]`),
-  and one store of an epilogue of `acc` into `c[rows, cols]` -> `krn_gemm_nt` with bf16/f16 (32x32x16 MFMA), fp8
-  e4m3 (32x32x64 f8f6f4 MFMA) or int8 (32x32x32 i8 MFMA) operands. The epilogue may multiply or add float32
-  scalars, per-row vectors (`s[rows, 0:1]`) and per-column vectors (`s[0:1, cols]`), in the program's order, each
-  rounded to float32, then convert to bf16/f16/f32 (or keep int32). The kernel picks its own tile sizes for 256 CUs;
+  and one store of an epilogue of `acc` into `c[rows, cols]` (after any `acc = f(acc)` steps) -> `krn_gemm_nt` with
+  bf16/f16 (32x32x16 MFMA), fp8 e4m3 (32x32x64 f8f6f4 MFMA) or int8 (32x32x32 i8 MFMA) operands. The epilogue may
+  multiply or add float32 scalars, per-row vectors (`s[rows, 0:1]`) and per-column vectors (`s[0:1, cols]`, or a
+  bias `v[cols]` of f32/f16/bf16), and apply relu, gelu or silu, in the program's order, each rounded to float32,
+  then convert to bf16/f16/f32 (or keep int32). The kernel picks its own tile sizes for 256 CUs;
   the program's `bm, bn, bk` change only the grid it asks for, which must cover the output.
 * `AttentionPlan`: krn's flash-attention tile program (reference examples/04_libraries/08_flash_attention.py:35-59)
   with head dimension 64 or 128, f16 or bf16, causal or not -> `krn_attention_fwd`.
@@ -17,18 +18,20 @@ Replaces the reference's compile-checked HIP renderer (src/krn/compiler/hip.py:2
 f16/bf16 MFMA only, refused fp8 (compiler/matrix.py:129-139) and had no int8 product.
 """
 
+import dataclasses
 from dataclasses import dataclass, field
 
 from krn_amd.compiler import ir
 from krn_amd.dtypes import BF16, F8E4M3, F16, F32, I8, I32, PY_INT, Dtype
 
 GEMM_OPERANDS = (BF16, F16, F8E4M3, I8)
+ACTIVATIONS = {ir.Fn.RELU: "relu", ir.Fn.GELU: "gelu", ir.Fn.SILU: "silu"}
 
 
 @dataclass(frozen=True)
 class EpilogueOp:
-    """One elementwise step after the product: `op` is "mul" or "add"; the operand is a scalar expression, or a
-    row/column vector read from `tensor` (shape (M, 1) or (1, N))."""
+    """One elementwise step after the product: `op` is "mul" or "add" with a scalar expression or a row/column vector
+    read from `tensor` (shape (M, 1), (1, N) or (N,)), or the activation "relu", "gelu" or "silu"."""
 
     op: str
     scalar: ir.Expr | None = None
@@ -85,11 +88,41 @@ def _k_slice(s: ir.SliceExpr, var: ir.Var, bk: int) -> bool:
     return isinstance(s.start, ir.Var) and s.start == var and s.extent == bk and not s.squeeze
 
 
+def _substitute(e, var: ir.Var, value: ir.Expr):
+    """`e` with every use of the tile variable `var` replaced by `value`."""
+    if e == var:
+        return value
+    if not dataclasses.is_dataclass(e) or isinstance(e, type):
+        return e
+    changes = {}
+    for f in dataclasses.fields(e):
+        old = getattr(e, f.name)
+        if isinstance(old, tuple):
+            new = tuple(_substitute(x, var, value) for x in old)
+        elif dataclasses.is_dataclass(old) and not isinstance(old, type):
+            new = _substitute(old, var, value)
+        else:
+            continue
+        if new is not old and new != old:
+            changes[f.name] = new
+    return dataclasses.replace(e, **changes) if changes else e
+
+
 def match_gemm(kernel: ir.Kernel) -> GemmPlan | None:
     body = kernel.body
-    if len(body) != 3:
+    if len(body) < 3:
         return None
-    init, loop, store = body
+    init, loop, *post, store = body
+    # `acc = f(acc)` steps after the loop (bias, activations) fold into the stored expression
+    for statement in post:
+        if not (isinstance(statement, ir.TileAssign) and isinstance(init, ir.TileAssign) and
+                statement.var == init.var):
+            return None
+    if post and isinstance(store, ir.TileStore):
+        value = init.var
+        for statement in post:
+            value = _substitute(statement.value, init.var, value)
+        store = dataclasses.replace(store, value=_substitute(store.value, init.var, value))
     if not (isinstance(init, ir.TileAssign) and isinstance(init.value, ir.Zeros)):
         return None
     acc = init.var
@@ -154,6 +187,9 @@ def _epilogue(e: ir.Expr, acc: ir.Var, bm: int, bn: int) -> list[EpilogueOp] | N
         return [] if acc.dtype == F32 else None
     if isinstance(e, ir.Cast) and e.operand == acc and acc.dtype == I32 and e.dtype == F32:
         return []
+    if isinstance(e, ir.Math) and e.fn in ACTIVATIONS and e.dtype == F32 and len(e.args) == 1:
+        chain = _epilogue(e.args[0], acc, bm, bn)
+        return None if chain is None else [*chain, EpilogueOp(ACTIVATIONS[e.fn])]
     if isinstance(e, ir.Binary) and e.op in (ir.Op.MUL, ir.Op.ADD) and e.dtype == F32:
         for inner, other in ((e.lhs, e.rhs), (e.rhs, e.lhs)):
             chain = _epilogue(inner, acc, bm, bn)
@@ -168,11 +204,16 @@ def _epilogue(e: ir.Expr, acc: ir.Var, bm: int, bn: int) -> list[EpilogueOp] | N
 
 
 def _operand(e: ir.Expr, bm: int, bn: int) -> tuple | None:
-    """A scalar float32 expression over parameters and constants, or a row/column vector tile load."""
+    """A scalar float32 expression over parameters and constants, or a row/column vector tile load: a (bm, 1) or
+    (1, bn) slice of a float32 matrix, or the `v[cols]` slice of a float32/f16/bf16 vector widened to float32."""
     if not e.shape:
         if _scalar_expr(e) and e.dtype == F32:
             return (e, None, "")
         return None
+    vector = e.operand if isinstance(e, ir.Cast) and e.dtype == F32 else e
+    if isinstance(vector, ir.TileLoad) and vector.tensor.type.rank == 1 and vector.shape == (bn,) and \
+            vector.dtype in (F32, F16, BF16) and _block_slice(vector.slices[0], "x") == bn:
+        return (None, vector.tensor.name, "col")
     if isinstance(e, ir.TileLoad) and e.dtype == F32 and e.tensor.type.rank == 2 and len(e.shape) == 2:
         rows, cols = e.slices
         if e.shape == (bm, 1) and _block_slice(rows, "y") == bm and isinstance(cols.start, ir.Const) and \

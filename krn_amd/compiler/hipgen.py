@@ -75,12 +75,18 @@ __device__ __forceinline__ unsigned char k8enc(float x) {
 }
 __device__ __forceinline__ float kmax(float a, float b) { return a != a ? a : b != b ? b : a > b ? a : b; }
 __device__ __forceinline__ float kmin(float a, float b) { return a != a ? a : b != b ? b : a < b ? a : b; }
+// activations as krn states them (reference compiler/emit.py:112-114)
+__device__ __forceinline__ float krelu(float x) { return x < 0.0f ? 0.0f : x; }
+__device__ __forceinline__ float kgelu(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }
+__device__ __forceinline__ float ksilu(float x) { return x / (1.0f + expf(-x)); }
 """
 
 MATH = {
     ir.Fn.EXP: "expf({0})", ir.Fn.EXP2: "exp2f({0})", ir.Fn.LOG: "logf({0})", ir.Fn.LOG2: "log2f({0})",
     ir.Fn.SQRT: "sqrtf({0})", ir.Fn.RSQRT: "(1.0f / sqrtf({0}))", ir.Fn.ABS: "fabsf({0})", ir.Fn.TANH: "tanhf({0})",
-    ir.Fn.RELU: "kmax({0}, 0.0f)", ir.Fn.MAXIMUM: "kmax({0}, {1})", ir.Fn.MINIMUM: "kmin({0}, {1})",
+    ir.Fn.RELU: "krelu({0})", ir.Fn.GELU: "kgelu({0})", ir.Fn.SILU: "ksilu({0})",
+    ir.Fn.SIGMOID: "(1.0f / (1.0f + expf(-({0}))))", ir.Fn.ERF: "erff({0})",
+    ir.Fn.MAXIMUM: "kmax({0}, {1})", ir.Fn.MINIMUM: "kmin({0}, {1})",
 }  # fmt: skip
 
 
@@ -119,9 +125,11 @@ class Emitter:
 
     @staticmethod
     def index(idx: list[str], of: tuple[int, ...]) -> str:
+        """Linear index into a tile of shape `of` broadcast numpy-style (aligned from the right) to the loop `idx`."""
         if not of:
             return "0"
-        terms = [f"{idx[a]} * {math.prod(of[a + 1:])}" for a, extent in enumerate(of) if extent != 1]
+        skip = len(idx) - len(of)
+        terms = [f"{idx[a + skip]} * {math.prod(of[a + 1:])}" for a, extent in enumerate(of) if extent != 1]
         return " + ".join(terms) or "0"
 
     def emit(self) -> tuple[str, int]:

@@ -42,6 +42,10 @@ class Fn(Enum):
     ABS = "abs"
     TANH = "tanh"
     RELU = "relu"
+    GELU = "gelu"
+    SILU = "silu"
+    SIGMOID = "sigmoid"
+    ERF = "erf"
     MAXIMUM = "maximum"
     MINIMUM = "minimum"
 

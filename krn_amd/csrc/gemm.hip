@@ -23,15 +23,33 @@
 
 namespace krn {
 
-enum Op : int { MUL_SCALAR = 0, MUL_ROW = 1, MUL_COL = 2, ADD_SCALAR = 3, ADD_ROW = 4, ADD_COL = 5 };
+// Epilogue operations. Codes 0-5 take a float32 scalar or a row/column vector; 6-8 are the activations of krn's
+// `lib.matmul` (reference src/krn/lib/lib_kernels.py:31-48, formulas of compiler/emit.py:112-114). A vector's
+// element kind rides in bits 4-5 of the code: 0 float32, 1 f16, 2 bf16.
+enum Op : int {
+  MUL_SCALAR = 0, MUL_ROW = 1, MUL_COL = 2, ADD_SCALAR = 3, ADD_ROW = 4, ADD_COL = 5, RELU = 6, GELU = 7, SILU = 8
+};
+constexpr int VEC_KIND_SHIFT = 4;
 
 struct Epilogue {
   int out_kind;          // F32, F16, BF16 or I32 (I32 only for an int8 product with no operations)
   int nops;              // elementwise operations applied in order, each rounded to float32
   int op[4];
   float scalar[4];
-  const float* vec[4];   // per-row (length M) or per-column (length N) vectors
+  const void* vec[4];    // per-row (length M) or per-column (length N) vectors
 };
+
+__device__ __forceinline__ float vec_at(const void* v, int kind, int64_t i) {
+  if (kind == 1) return h2f(static_cast<const uint16_t*>(v)[i]);
+  if (kind == 2) return bf2f(static_cast<const uint16_t*>(v)[i]);
+  return static_cast<const float*>(v)[i];
+}
+
+__device__ __forceinline__ float activation(int op, float x) {
+  if (op == RELU) return x < 0.0f ? 0.0f : x;
+  if (op == GELU) return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, erff(__fmul_rn(x, 0.7071067811865476f))));
+  return __fdiv_rn(x, __fadd_rn(1.0f, expf(-x)));  // SILU
+}
 
 enum Format : int { FMT_BF16 = 0, FMT_F16 = 1, FMT_I8 = 2, FMT_FP8 = 3 };
 
@@ -131,18 +149,21 @@ __device__ __forceinline__ void store_block(const V& block, uint32_t* patch, voi
 #pragma unroll
   for (int c = 0; c < 16; ++c) v[c] = INT ? (float)(int32_t)bits[c] : __uint_as_float(bits[c]);
   for (int i = 0; i < e.nops; ++i) {
-    const int op = e.op[i];
-    if (op % 3 == 0) {
+    const int op = e.op[i] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[i] >> VEC_KIND_SHIFT;
+    if (op >= RELU) {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) v[c] = activation(op, v[c]);
+    } else if (op % 3 == 0) {
 #pragma unroll
       for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], e.scalar[i]) : __fadd_rn(v[c], e.scalar[i]);
     } else if (op % 3 == 1) {
-      const float s = e.vec[i][m];
+      const float s = vec_at(e.vec[i], kind, m);
 #pragma unroll
       for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], s) : __fadd_rn(v[c], s);
     } else {
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
-        const float s = n + c < N ? e.vec[i][n + c] : 0.0f;
+        const float s = n + c < N ? vec_at(e.vec[i], kind, n + c) : 0.0f;
         v[c] = op < 3 ? __fmul_rn(v[c], s) : __fadd_rn(v[c], s);
       }
     }
@@ -723,7 +744,7 @@ extern "C" {
 
 // See include/krn_amd.h for the contract of each entry point.
 int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n, int64_t k,
-                int nops, const int* ops, const float* scalars, const float* const* vectors, void* stream) {
+                int nops, const int* ops, const float* scalars, const void* const* vectors, void* stream) {
   Epilogue e{};
   e.out_kind = out_kind;
   if (nops < 0 || nops > 4) {
@@ -735,11 +756,12 @@ int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind
     e.op[i] = ops[i];
     e.scalar[i] = scalars ? scalars[i] : 0.0f;
     e.vec[i] = vectors ? vectors[i] : nullptr;
-    if (ops[i] < 0 || ops[i] > 5) {
+    const int op = ops[i] & ((1 << VEC_KIND_SHIFT) - 1), kind = ops[i] >> VEC_KIND_SHIFT;
+    if (ops[i] < 0 || op > SILU || kind > 2 || (kind != 0 && (op >= RELU || op % 3 == 0))) {
       krn_set_error("gemm: unknown epilogue operation %d", ops[i]);
       return -1;
     }
-    if (ops[i] % 3 != 0 && e.vec[i] == nullptr) {
+    if (op < RELU && op % 3 != 0 && e.vec[i] == nullptr) {
       krn_set_error("gemm: epilogue operation %d needs a vector", i);
       return -1;
     }

@@ -238,15 +238,19 @@ class Launch:
             return False  # not the whole product: the generic lowering keeps the program's exact meaning
         ops = []
         for op in plan.ops:
+            if op.op in library.ACTIVATIONS:
+                ops.append((library.ACTIVATIONS[op.op], 0.0, 0))
+                continue
             base = library.MUL_SCALAR if op.op == "mul" else library.ADD_SCALAR
             if op.tensor is None:
                 ops.append((base, float(_scalar_value(op.scalar, params)), 0))
             else:
                 vector = params[op.tensor]
-                want = (m, 1) if op.axis == "row" else (1, n)
-                if vector.shape != want:
+                wants = [(m, 1)] if op.axis == "row" else [(1, n), (n,)]
+                if vector.shape not in wants or vector.dtype not in library.VECTOR_KINDS:
                     return False
-                ops.append((base + (1 if op.axis == "row" else 2), 0.0, vector.pointer))
+                code = base + (1 if op.axis == "row" else 2) + library.VECTOR_KINDS[vector.dtype]
+                ops.append((code, 0.0, vector.pointer))
         if plan.layout == "nn":
             scratch = self.device_scratch(stream, n * k * 2)
             library.transpose16(b.pointer, scratch.pointer, k, n, stream.handle)

@@ -15,6 +15,8 @@ are decoded exactly to float32 first, and int8 operands accumulate exactly in in
 
 from collections.abc import Sequence
 
+import math
+
 import numpy as np
 
 from krn_amd.compiler import ir
@@ -279,10 +281,16 @@ TILE_OPS = {
     ir.Op.LT: np.less, ir.Op.LE: np.less_equal, ir.Op.GT: np.greater, ir.Op.GE: np.greater_equal,
     ir.Op.EQ: np.equal, ir.Op.NE: np.not_equal, ir.Op.AND: np.logical_and, ir.Op.OR: np.logical_or,
 }  # fmt: skip
+_erf = np.vectorize(math.erf, otypes=[np.float64])
 MATH = {
     ir.Fn.EXP: np.exp, ir.Fn.EXP2: np.exp2, ir.Fn.LOG: np.log, ir.Fn.LOG2: np.log2, ir.Fn.SQRT: np.sqrt,
     ir.Fn.RSQRT: lambda x: 1 / np.sqrt(x), ir.Fn.ABS: np.abs, ir.Fn.TANH: np.tanh,
     ir.Fn.RELU: lambda x: np.maximum(x, 0), ir.Fn.MAXIMUM: np.maximum, ir.Fn.MINIMUM: np.minimum,
+    # reference emulator/emulate.py:373-384: erf in float64 rounded to the operand's type, the rest in that type
+    ir.Fn.ERF: lambda x: _erf(x).astype(x.dtype),
+    ir.Fn.GELU: lambda x: x.dtype.type(0.5) * x * (x.dtype.type(1) + _erf(x * x.dtype.type(0.7071067811865476)).astype(x.dtype)),
+    ir.Fn.SILU: lambda x: x / (x.dtype.type(1) + np.exp(-x)),
+    ir.Fn.SIGMOID: lambda x: x.dtype.type(1) / (x.dtype.type(1) + np.exp(-x)),
 }  # fmt: skip
 
 

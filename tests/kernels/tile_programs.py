@@ -3,10 +3,12 @@
 `matmul` and `flash_attention` are krn's own example programs (reference examples/04_libraries/01_gemm_tiles.py:34-40
 and 08_flash_attention.py:35-59), restated here because the kernels must be the same programs; `gemm_nt` is the
 `C = A @ B^T` form of the benchmark configuration, and the quantized GEMMs add the scale epilogues. The small tile
-kernels mirror the operations of reference tests/kernels/tile_ops.py.
+kernels mirror the operations of reference tests/kernels/tile_ops.py. `matmul_epilogue` is the kernel behind krn's
+`lib.matmul` (reference src/krn/lib/lib_kernels.py:20-48); the reference declares it generic over F with Python
+3.12 syntax, so it is stated here once per dtype it runs with (f16 and f32).
 """
 
-from krn_amd import Const, Matrix, T, Tensor, arange, block, kernel, pipelined, struct, where, zeros
+from krn_amd import Const, Matrix, T, Tensor, Vector, arange, block, kernel, pipelined, struct, where, zeros
 
 
 @struct
@@ -229,3 +231,52 @@ def matmul_f16_f32(t: Tiling, a: Matrix[T.f16], b: Matrix[T.f16], c: Matrix[T.f3
     for ks in pipelined(a.shape[1], t.bk):
         acc += a[rows, ks] @ b[ks, cols]
     c[rows, cols] = acc
+
+
+@struct
+class MatmulTiling:
+    bm: Const[int] = 16
+    bn: Const[int] = 16
+    bk: Const[int] = 8
+    bias: Const[bool] = False
+    relu: Const[bool] = False
+    gelu: Const[bool] = False
+    silu: Const[bool] = False
+
+
+@kernel
+def matmul_epilogue(
+    t: MatmulTiling, a: Matrix[T.f16], b: Matrix[T.f16], bias: Vector[T.f16], out: Matrix[T.f16]
+) -> None:
+    rows, cols = block.tile(t.bm, t.bn)
+    acc = zeros(T.f32, t.bm, t.bn)
+    for ks in pipelined(a.shape[1], t.bk):
+        acc += a[rows, ks] @ b[ks, cols]
+    if t.bias:
+        acc += bias[cols].to(T.f32)
+    if t.relu:
+        acc = acc.relu()
+    if t.gelu:
+        acc = acc.gelu()
+    if t.silu:
+        acc = acc.silu()
+    out[rows, cols] = acc.to(out.dtype)
+
+
+@kernel
+def matmul_epilogue_f32(
+    t: MatmulTiling, a: Matrix[T.f32], b: Matrix[T.f32], bias: Vector[T.f32], out: Matrix[T.f32]
+) -> None:
+    rows, cols = block.tile(t.bm, t.bn)
+    acc = zeros(T.f32, t.bm, t.bn)
+    for ks in pipelined(a.shape[1], t.bk):
+        acc += a[rows, ks] @ b[ks, cols]
+    if t.bias:
+        acc += bias[cols].to(T.f32)
+    if t.relu:
+        acc = acc.relu()
+    if t.gelu:
+        acc = acc.gelu()
+    if t.silu:
+        acc = acc.silu()
+    out[rows, cols] = acc.to(out.dtype)

@@ -1,0 +1,47 @@
+"""Host-side lowering (no GPU): which gfx950 plan each tile program gets, and the epilogue chain the GEMM plan
+carries to krn_gemm_nt."""
+
+import pytest
+
+from krn_amd.compiler import cdna4
+from krn_amd.compiler.capture import capture
+from tests.conftest import KERNELS
+
+BASE = {"bm": 16, "bn": 16, "bk": 8, "bias": False, "relu": False, "gelu": False, "silu": False}
+# reference src/krn/lib/lib_ours.py:38-46: the constants each lib.matmul epilogue sets
+EPILOGUES = {
+    "none": {}, "bias": {"bias": True}, "relu": {"relu": True}, "gelu": {"gelu": True},
+    "bias_relu": {"bias": True, "relu": True}, "bias_gelu": {"bias": True, "gelu": True}, "silu": {"silu": True},
+}  # fmt: skip
+
+
+@pytest.mark.parametrize("name", list(EPILOGUES))
+def test_lib_matmul_f16_lowers_to_the_mfma_gemm_with_its_epilogue(name):
+    flags = EPILOGUES[name]
+    plan = cdna4.lower(capture(KERNELS, "matmul_epilogue", consts={"t": {**BASE, **flags}}))
+    assert isinstance(plan, cdna4.GemmPlan)
+    assert plan.layout == "nn" and plan.c == "out"
+    want = []
+    if flags.get("bias"):
+        want.append(("add", "bias", "col"))
+    want += [(act, None, "") for act in ("relu", "gelu", "silu") if flags.get(act)]
+    assert [(op.op, op.tensor, op.axis) for op in plan.ops] == want
+
+
+def test_lib_matmul_f32_has_no_matrix_unit_product_and_lowers_generically():
+    plan = cdna4.lower(capture(KERNELS, "matmul_epilogue_f32", consts={"t": {**BASE, "bias": True, "gelu": True}}))
+    assert isinstance(plan, cdna4.GenericPlan)
+
+
+@pytest.mark.parametrize("name, kind", [("gemm_nt", cdna4.GemmPlan), ("gemm_fp8", cdna4.GemmPlan),
+                                        ("gemm_w8a8", cdna4.GemmPlan), ("gemm_i8_i32", cdna4.GemmPlan),
+                                        ("matmul", cdna4.GemmPlan), ("row_softmax", cdna4.GenericPlan)])
+def test_plan_kinds(name, kind):
+    consts = {"t": {"bm": 64, "bn": 64, "bk": 32}} if kind is cdna4.GemmPlan else {"t": {"rows": 8, "cols": 16}}
+    assert isinstance(cdna4.lower(capture(KERNELS, name, consts=consts)), kind)
+
+
+def test_attention_program_lowers_to_the_attention_kernel():
+    consts = {"t": {"bq": 64, "bk": 64, "d": 128, "causal": True}}
+    plan = cdna4.lower(capture(KERNELS, "flash_attention_bf16", consts=consts))
+    assert isinstance(plan, cdna4.AttentionPlan) and plan.d == 128 and plan.causal
