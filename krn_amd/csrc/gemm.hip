@@ -3,9 +3,10 @@
 // This is the lowering of krn's tile contraction `acc += a[rows, ks] @ b[cols, ks].transpose()` followed by
 // `c[rows, cols] = f(acc).to(dtype)` (reference compiler/ir.py:309-315 Accumulate, compiler/emit.py:788-821). One
 // workgroup owns a BM x BN output tile, four waves split it 2 x 2, and every wave keeps its accumulators in
-// registers as 32x32 MFMA blocks. Two main loops: `gemm_pipe` for whole 256 x 256 tiles (a ring of direct-to-LDS
-// slices, see there) and `gemm_tile` for ragged shapes (128-byte slices staged through registers, bounds-checked,
-// double buffered). Both end in the same epilogue, `store_block`.
+// registers as 32x32 MFMA blocks. Main loops: `gemm_pipe` (bf16/f16/int8) and `gemm_pp` (fp8) for whole 256 x 256
+// tiles (rings of direct-to-LDS slices, see there), `gemm_skinny` for M <= 128, and `gemm_tile` for ragged shapes
+// (128-byte slices staged through registers, bounds-checked, double buffered). All end in the same epilogue,
+// `patch_put` + `patch_store`.
 //
 // One byte-oriented main loop serves three operand formats, because each MFMA consumes the same 16 bytes per lane
 // per half-wave:
@@ -109,9 +110,10 @@ struct Mfma<FMT_FP8> {
 constexpr int PATCH_STRIDE = 36;
 constexpr int PATCH_WORDS = 32 * PATCH_STRIDE;
 
+// Register half: copy one accumulator block into the wave's patch. Small and fully unrolled, so that the
+// accumulator index is a constant and the accumulators never leave registers.
 template <bool INT, typename V>
-__device__ __forceinline__ void store_block(const V& block, uint32_t* patch, void* C, int64_t ldc, int64_t row0,
-                                            int64_t col0, int64_t M, int64_t N, const Epilogue& e, int lane) {
+__device__ __forceinline__ void patch_put(const V& block, uint32_t* patch, int lane) {
   const int half = lane >> 5, r32 = lane & 31;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -120,6 +122,12 @@ __device__ __forceinline__ void store_block(const V& block, uint32_t* patch, voi
     else
       patch[((r >> 2) * 8 + half * 4 + (r & 3)) * PATCH_STRIDE + r32] = __float_as_uint(block[r]);
   }
+}
+
+// Memory half: the patch through the epilogue to C.
+template <bool INT>
+__device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int64_t ldc, int64_t row0, int64_t col0,
+                                                   int64_t M, int64_t N, const Epilogue& e, int lane) {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the patch is written before any lane reads it
   __builtin_amdgcn_wave_barrier();
   const int rr = lane >> 1, c0 = (lane & 1) * 16;
@@ -191,6 +199,24 @@ __device__ __forceinline__ void store_block(const V& block, uint32_t* patch, voi
   } else {
     for (int c = 0; c < 16 && n + c < N; ++c) out[c] = (uint16_t)(h[c >> 1] >> ((c & 1) * 16));
   }
+}
+
+template <bool INT>
+__device__ __noinline__ void patch_store(uint32_t* patch, void* C, int64_t ldc, int64_t row0, int64_t col0, int64_t M,
+                                         int64_t N, const Epilogue& e, int lane) {
+  patch_store_inline<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
+}
+
+// One accumulator block to C. Tiles with many blocks per wave call the out-of-line store (their loop over blocks
+// must unroll completely); the skinny kernel, with at most four blocks, inlines it.
+template <bool INT, bool INLINE = false, typename V>
+__device__ __forceinline__ void store_block(const V& block, uint32_t* patch, void* C, int64_t ldc, int64_t row0,
+                                            int64_t col0, int64_t M, int64_t N, const Epilogue& e, int lane) {
+  patch_put<INT>(block, patch, lane);
+  if constexpr (INLINE)
+    patch_store_inline<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
+  else
+    patch_store<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
 }
 
 // 16 bytes of row `base` starting at byte `kb`, zero past the row's end or for a row outside the matrix. VEC: the
@@ -541,6 +567,152 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
                                  n0 + wn * (BN / WN) + j * 32, M, N, e, lane);
 }
 
+// Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
+// 32x32x32 steps, fp8: one 32x32x64 step per slice -- 512 MFMA cycles per wave in every format). Eight waves form two
+// groups of four: group g owns rows [128 g, 128 g + 128) of the tile, and within a group wave q owns the 64 x 128
+// block (q >> 1, q & 1). Waves w and w + 4 run on the same SIMD, and group 1 starts one barrier late, so on every
+// SIMD one wave issues its 16 MFMAs while the other reads its next fragments from LDS and issues direct-to-LDS loads:
+// the matrix core is fed from one wave while the other's LDS and memory waits are hidden behind it.
+//
+// Every slot ends in a workgroup barrier. Per slice j a wave runs a memory phase (issue its part of the loads of
+// slice j + STAGES - 1, read the fragments of slice j, wait for them and for its own loads of slice j + 1) and then
+// a compute phase (the MFMAs of slice j). Group 0 loads the A rows of every slice, group 1 the B rows. Slice j is
+// read by group 0 in slot 2j and by group 1 in slot 2j + 1, so its stage is free from slot 2j + 2 on, which is when
+// the loads of slice j + STAGES (same stage) are issued at the earliest.
+template <int FMT, int STAGES>
+__global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                                                  void* __restrict__ C, int64_t M, int64_t N, int64_t kbytes,
+                                                  int64_t lda, int64_t ldb, int64_t ldc, Epilogue e) {
+  typedef Mfma<FMT> Unit;
+  typedef typename Unit::Acc Acc;
+  constexpr int BM = 256, BN = 256, BKB = 64, CPR = 4;  // 64-byte slice rows of four 16-byte chunks
+  constexpr int TM = 2, TN = 4;                          // 32x32 blocks per wave
+  constexpr int STEP = Unit::kBytes, CH = STEP / 32, KS = BKB / STEP;
+  constexpr int PART = BM * BKB;                         // bytes of one operand's rows in a stage (16 KiB)
+  constexpr int STAGE_BYTES = 2 * PART;
+  constexpr int LOADS = PART / 1024 / 4;                 // 1 KiB wave loads per wave per slice (4)
+  constexpr int VMWAIT = (STAGES - 2) * LOADS;
+  static_assert(STAGES >= 3 && STAGES * STAGE_BYTES <= 160 * 1024, "LDS of one CU");
+  static_assert(VMWAIT <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * STAGE_BYTES];
+
+  int tm, tn;
+  tile_of((int)(M / BM), (int)(N / BN), tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = wave >> 2, q = wave & 3;
+  const int half = lane >> 5, r32 = lane & 31;
+
+  // loads: group 0 fills the A part of a stage, group 1 the B part; wave q the rows [64 q, 64 q + 64)
+  const int lrow = lane / CPR, lslot = lane % CPR;
+  const uint8_t* src[LOADS];
+  {
+    const uint8_t* base = g ? B + n0 * ldb : A + m0 * lda;
+    const int64_t ld = g ? ldb : lda;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int row = (q * LOADS + j) * 16 + lrow;
+      src[j] = base + row * ld + (lslot ^ swz4(row)) * 16;
+    }
+  }
+  const int dst0 = g * PART + q * LOADS * 1024;
+  // fragment offsets (16-byte units within a stage)
+  const int wr = g * 128 + (q >> 1) * 64, wc = (q & 1) * 128;
+  int a_off[TM][KS][CH], b_off[TN][KS][CH];
+#pragma unroll
+  for (int k = 0; k < KS; ++k)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int chunk = (k * STEP + half * (STEP / 2)) / 16 + c;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wr + i * 32 + r32;
+        a_off[i][k][c] = row * CPR + (chunk ^ swz4(row));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = wc + j * 32 + r32;
+        b_off[j][k][c] = BM * CPR + row * CPR + (chunk ^ swz4(row));
+      }
+    }
+  const int nk = (int)(kbytes / BKB);
+
+#define KRN_ISSUE(slice)                                                                                        \
+  do {                                                                                                          \
+    uint8_t* stage = lds + ((slice) % STAGES) * STAGE_BYTES + dst0;                                             \
+    const int64_t koff = (int64_t)(slice) * BKB;                                                                \
+    _Pragma("unroll") for (int j = 0; j < LOADS; ++j) __builtin_amdgcn_global_load_lds(                         \
+        (const void*)(src[j] + koff), (__attribute__((address_space(3))) void*)(stage + j * 1024), 16, 0, 0);   \
+  } while (0)
+#define KRN_VMWAIT(n) __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | ((n) & 15) | (((n) >> 4) << 14))
+#define KRN_LGKWAIT() __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00)
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nk) KRN_ISSUE(s);
+  Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = Acc{};
+  if (nk > STAGES - 2) {
+    KRN_VMWAIT(VMWAIT);
+  } else {
+    KRN_VMWAIT(0);
+  }
+  __builtin_amdgcn_s_barrier();
+  if (g == 1) __builtin_amdgcn_s_barrier();
+  u32x4 fa[KS][TM][CH], fb[KS][TN][CH];
+  for (int kt = 0; kt < nk; ++kt) {
+    // memory phase
+    const bool refill = kt + STAGES - 1 < nk;
+    if (refill) KRN_ISSUE(kt + STAGES - 1);
+    {
+      const u32x4* st = reinterpret_cast<const u32x4*>(lds + (kt % STAGES) * STAGE_BYTES);
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int c = 0; c < CH; ++c) fa[k][i][c] = st[a_off[i][k][c]];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int c = 0; c < CH; ++c) fb[k][j][c] = st[b_off[j][k][c]];
+      }
+    }
+    KRN_LGKWAIT();
+    if (refill) {
+      KRN_VMWAIT(VMWAIT);
+    } else {
+      KRN_VMWAIT(0);
+    }
+    __builtin_amdgcn_s_barrier();
+    // compute phase
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) Unit::step(acc[i][j], fa[k][i], fb[k][j]);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+  }
+  if (g == 0) __builtin_amdgcn_s_barrier();
+#undef KRN_ISSUE
+#undef KRN_VMWAIT
+#undef KRN_LGKWAIT
+  __syncthreads();  // every wave is done with the ring before its LDS becomes the store patches
+
+  uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      store_block<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wr + i * 32, n0 + wc + j * 32, M, N, e, lane);
+}
+
 // Skinny products (M <= 128), the HBM-bound shapes: B (N x K) is streamed once and A is small enough to be served
 // from L2. A workgroup owns 32 output columns and all M rows (MT blocks of 32); its WAVES waves split K, wave w
 // taking the 128-byte K slices w, w + WAVES, ..., so that together they read WAVES * 128 contiguous bytes of each
@@ -618,7 +790,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __re
   }
   __syncthreads();
   if (wave < MT)
-    store_block<FMT == FMT_I8>(sum, lds + wave * PATCH_WORDS, C, ldc, (int64_t)wave * 32, n0, M, N, e, lane);
+    store_block<FMT == FMT_I8, true>(sum, lds + wave * PATCH_WORDS, C, ldc, (int64_t)wave * 32, n0, M, N, e, lane);
 }
 
 }  // namespace krn
@@ -673,6 +845,24 @@ static int launch_pipe(const void* a, const void* b, void* c, int64_t m, int64_t
   return 0;
 }
 
+template <int FMT, int STAGES>
+static int launch_pp(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                     int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+  const int64_t tiles = (m / 256) * (n / 256);
+  if (tiles > 0x7fffffff) {
+    krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
+    return -1;
+  }
+  hipLaunchKernelGGL((gemm_pp<FMT, STAGES>), dim3((unsigned)tiles), dim3(512), 0, stream, (const uint8_t*)a,
+                     (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    krn_set_error("gemm launch: %s", hipGetErrorString(err));
+    return (int)err;
+  }
+  return 0;
+}
+
 template <int FMT, int MT>
 static int launch_skinny_mt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                             int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
@@ -701,13 +891,17 @@ static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64
   return -1;
 }
 
-// Whole 256 x 256 tiles: for bf16/f16 a ring of four 64-byte K slices (two MFMA steps each); for fp8 and int8 two
-// 128-byte slices (two fp8 or four int8 MFMA steps each).
+// Whole 256 x 256 tiles: for bf16/f16 a ring of four 64-byte K slices (two MFMA steps each); for fp8 the ping-pong
+// ring of four 64-byte slices (one MFMA step each); for int8 two 128-byte slices (four MFMA steps each).
 template <int FMT>
 static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  // eight waves (4 x 2, each 64 x 128 of the tile): two waves per SIMD hide each other's LDS and barrier waits
-  if constexpr (FMT == FMT_FP8 || FMT == FMT_I8)
+  // fp8: the ping-pong loop (one 64x64 f8f6f4 MFMA step per 64-byte slice keeps its memory phase short enough to
+  // hide behind the other group's MFMAs). bf16/f16 and int8: eight waves (4 x 2, each 64 x 128 of the tile) that
+  // interleave their own LDS reads with their MFMAs.
+  if constexpr (FMT == FMT_FP8)
+    return launch_pp<FMT, 4>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  else if constexpr (FMT == FMT_I8)
     return launch_pipe<FMT, 256, 256, 4, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   else
     return launch_pipe<FMT, 256, 256, 4, 2, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
