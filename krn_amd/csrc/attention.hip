@@ -10,8 +10,10 @@
 // computes the transposed products S^T = K Q^T and O^T += V^T P^T with v_mfma_f32_32x32x16_{bf16,f16}. In that form
 // every lane holds one query row (lane & 31) and 16 of the keys of a 32-key block (its half-wave partner holds the
 // other 16), so the row maximum and sum are lane-local plus one exchange with lane ^ 32, the rescale of O is
-// lane-local, and P feeds the next MFMA straight from registers as its B operand. Q stays in registers for the
-// whole pass. K and V tiles of 64 keys stream through LDS (a ring of three K tiles and two V tiles) filled by
+// lane-local, and P feeds the next MFMA straight from registers as its B operand. The row maximum is exchanged with
+// v_permlane32_swap; each lane keeps its own part of the row sum, and the two parts are added once at the end (the
+// lazy rescale multiplies both by the same factor). Q stays in registers for the whole pass. K and V tiles of 64
+// keys stream through LDS (a ring of three K tiles and two V tiles) filled by
 // direct-to-LDS loads (global_load_lds_dwordx4); both keep the row-major [key][d] layout of global memory. K is read
 // as the A operand of S^T with 16-byte reads (chunk c of key row r at slot c ^ (r & 15)); V is read as the A
 // operand of O^T with ds_read_b64_tr_b16, which hands each lane four keys of one d column, so V never needs a
@@ -70,6 +72,12 @@ __device__ __forceinline__ int v_slot(int key, int chunk) {
   return D == 128 ? chunk ^ ((key & 3) << 2) : chunk ^ (((key >> 1) & 1) << 2);
 }
 
+// max(x, x of lane ^ 32): the two lanes that hold one query row (v_permlane32_swap, no LDS round trip)
+__device__ __forceinline__ float pair_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
 // `causal` is a run-time argument rather than a template parameter: both variants then get the same code and
 // register allocation, and a non-causal launch only sees its limits at +infinity.
 template <bool BF, int D>
@@ -107,6 +115,7 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
   f32x16 acc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
+  // m: the exponent base of this lane's row (shared with lane ^ 32); total: this lane's part of the row sum
   float m = -1.0e30f, total = 0.0f;
 
   const int64_t kend = causal ? min(sk, q0 + BQ) : sk;
@@ -126,18 +135,18 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
   // Each lane's element offsets inside a tile are fixed: computed once here; a load adds the tile's base (uniform)
   const int lrow = lane / DCH, lslot = lane % DCH;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  int koff[LOADS], voff[LOADS];
+  uint32_t koff[LOADS], voff[LOADS];  // byte offsets within a tile
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
     const int row = (wave * LOADS + j) * ROWS_PER_LOAD + lrow;
-    koff[j] = row * D + k_slot<D>(row, lslot) * 8;
-    voff[j] = row * D + v_slot<D>(row, lslot) * 8;
+    koff[j] = (uint32_t)(row * D + k_slot<D>(row, lslot) * 8) * 2;
+    voff[j] = (uint32_t)(row * D + v_slot<D>(row, lslot) * 8) * 2;
   }
 #define KRN_FA_LOAD(src, tile, base, OFF)                                                                     \
   do {                                                                                                        \
     const int64_t t0 = (int64_t)(tile) * BKEY;                                                                \
     if (t0 + BKEY <= sk) {                                                                                    \
-      const uint16_t* tb = (src) + t0 * D;                                                                    \
+      const uint8_t* tb = reinterpret_cast<const uint8_t*>((src) + t0 * D);                                   \
       _Pragma("unroll") for (int j = 0; j < LOADS; ++j) __builtin_amdgcn_global_load_lds(                     \
           (const void*)(tb + OFF[j]),                                                                         \
           (__attribute__((address_space(3))) void*)(lds + (base) + (wave_s * LOADS + j) * 1024), 16, 0, 0);   \
@@ -146,7 +155,7 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
         const int row = (wave * LOADS + j) * ROWS_PER_LOAD + lrow;                                            \
         const int64_t key = min(t0 + row, sk - 1);                                                            \
         __builtin_amdgcn_global_load_lds(                                                                     \
-            (const void*)((src) + key * D + (OFF[j] - row * D)),                                              \
+            (const void*)(reinterpret_cast<const uint8_t*>((src) + key * D) + (OFF[j] - row * D * 2)),                                              \
             (__attribute__((address_space(3))) void*)(lds + (base) + (wave_s * LOADS + j) * 1024), 16, 0, 0); \
       }                                                                                                       \
     }                                                                                                         \
@@ -171,7 +180,7 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
     float raw = S[0];                                                                                         \
     _Pragma("unroll") for (int r = 1; r < 16; ++r) raw = fmaxf(raw, S[r]);                                    \
     raw *= scale;                                                                                             \
-    out = fmaxf(raw, __shfl_xor(raw, 32));                                                                    \
+    out = pair_max(raw);                                                                                      \
   } while (0)
   // p = exp2(s * sc - m) in f32 for the row sum, packed to 16 bits as P^T, the B operand of two k16 steps
 #define KRN_FA_EXP(S, sc)                                                                                     \
@@ -249,7 +258,7 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
           SC[r] = x;                                                                                          \
           mx = fmaxf(mx, x);                                                                                  \
         }                                                                                                     \
-        tmax = fmaxf(mx, __shfl_xor(mx, 32));                                                                 \
+        tmax = pair_max(mx);                                                                                  \
       }                                                                                                       \
       /* Lazy rescale: the exponent base m only moves when some row maximum of the wave exceeds it by more    \
          than 8 (so every p <= 2^8); acc and total are then rescaled by exp2(m - m_new). A stale base scales  \
@@ -276,8 +285,7 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
         KRN_FA_EXP(SC, sc);                                                                                   \
         KRN_FA_PV(V_BASE + ((t) & 1) * TILE_BYTES, hb);                                                       \
       }                                                                                                       \
-      const float ps = psum[0] + psum[1];                                                                     \
-      total = total + (ps + __shfl_xor(ps, 32));                                                              \
+      total += psum[0] + psum[1];                                                                             \
     }                                                                                                         \
   } while (0)
 
@@ -300,6 +308,11 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
 #undef KRN_FA_PV
 #undef KRN_FA_HALF
 
+  // the row sum: this lane's 16 keys of every half plus those of its partner lane ^ 32
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(total), __float_as_uint(total), false, false);
+    total = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
   if (qrow < sq) {
 #pragma unroll
     for (int i = 0; i < D / 32; ++i)
