@@ -6,21 +6,22 @@
 // `o = (acc / total).to(dtype)`. Keys past the end of the sequence are invalid lanes: they take no part in the
 // maximum, the sum or the product.
 //
-// Layout (MI355X-first). A workgroup owns 128 query rows of one (batch, head); each of its 4 waves owns 32 rows and
+// Layout (MI355X-first). A workgroup owns 256 query rows of one (batch, head); each of its 8 waves owns 32 rows and
 // computes the transposed products S^T = K Q^T and O^T += V^T P^T with v_mfma_f32_32x32x16_{bf16,f16}. In that form
 // every lane holds one query row (lane & 31) and 16 of the keys of a 32-key block (its half-wave partner holds the
 // other 16), so the row maximum and sum are lane-local plus one exchange with lane ^ 32, the rescale of O is
 // lane-local, and P feeds the next MFMA straight from registers as its B operand. The row maximum is exchanged with
 // v_permlane32_swap; each lane keeps its own part of the row sum, and the two parts are added once at the end (the
 // lazy rescale multiplies both by the same factor). Q stays in registers for the whole pass. K and V tiles of 64
-// keys stream through LDS (a ring of three K tiles and two V tiles) filled by
-// direct-to-LDS loads (global_load_lds_dwordx4); both keep the row-major [key][d] layout of global memory. K is read
+// keys stream through LDS (a ring of three K tiles and two V tiles) filled by direct-to-LDS loads
+// (global_load_lds_dwordx4); both keep the row-major [key][d] layout of global memory. K is read
 // as the A operand of S^T with 16-byte reads (chunk c of key row r at slot c ^ (r & 15)); V is read as the A
 // operand of O^T with ds_read_b64_tr_b16, which hands each lane four keys of one d column, so V never needs a
 // transposing copy (chunk c of key row r at slot c ^ 4 (r & 3)). The key loop is software-pipelined in 32-key
 // halves: the score MFMAs of half h + 1 are issued before the exp2 / sum / pack of half h, so the matrix core and
-// the vector ALU of one wave work at the same time. Two workgroups share a CU, so each SIMD also interleaves two
-// waves. Causal launches run the late (long) query tiles of every head first.
+// the vector ALU of one wave work at the same time. Each SIMD interleaves two waves of the workgroup, and every K
+// and V tile loaded into LDS serves all 256 query rows (half the L2 traffic of 128-row workgroups). Causal launches
+// run the late (long) query tiles of every head first.
 //
 // Shortcuts. Exact: the row maximum of an unmasked half is taken on the raw scores and scaled once (rounding is
 // monotonic, scale > 0); halves wholly past a wave's last causal row are skipped (their p are exp2(-1e30 - m) = 0
@@ -28,6 +29,10 @@
 // unmasked halves, and the running maximum used as the exponent base is refreshed only when it is beaten by more
 // than 8 (p <= 2^8), which scales p, acc and total by the same power of two and leaves acc / total unchanged.
 #include "common.h"
+
+#ifndef KRN_FA_WAVES_DEFAULT
+#define KRN_FA_WAVES_DEFAULT 8
+#endif
 
 namespace krn {
 
@@ -57,7 +62,8 @@ struct Half<false> {
   }
 };
 
-constexpr int BQ = 128;   // query rows per workgroup
+constexpr int FA_WAVES = KRN_FA_WAVES_DEFAULT;  // waves per workgroup, 32 query rows each
+constexpr int BQ = 32 * FA_WAVES;               // query rows per workgroup
 constexpr int BKEY = 64;  // keys per LDS tile
 
 // LDS swizzles of the [key][d] tiles (64 banks serve 256 bytes per cycle). K: the 16-byte reads of 16 consecutive
@@ -81,7 +87,7 @@ __device__ __forceinline__ float pair_max(float x) {
 // `causal` is a run-time argument rather than a template parameter: both variants then get the same code and
 // register allocation, and a non-causal launch only sees its limits at +infinity.
 template <bool BF, int D>
-__global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+__global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attention_fwd(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                                                         const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
                                                         int64_t sq, int64_t sk, float scale, int q_tiles,
                                                         int causal) {
@@ -89,8 +95,8 @@ __global__ __launch_bounds__(256, 2) void attention_fwd(const uint16_t* __restri
   constexpr int DCH = D / 8;                // 16-byte chunks per key row
   constexpr int TILE_BYTES = BKEY * D * 2;  // one K (or V) tile
   constexpr int ROWS_PER_LOAD = 1024 / (D * 2);
-  constexpr int LOADS = BKEY / ROWS_PER_LOAD / 4;  // wave load instructions per tile, per operand
-  static_assert(LOADS * ROWS_PER_LOAD * 4 == BKEY, "whole wave loads");
+  constexpr int LOADS = BKEY / ROWS_PER_LOAD / FA_WAVES;  // wave load instructions per tile, per operand
+  static_assert(LOADS * ROWS_PER_LOAD * FA_WAVES == BKEY, "whole wave loads");
   static_assert(DCH <= 16, "swizzle range");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * TILE_BYTES];
 
@@ -334,7 +340,7 @@ template <bool BF, int D>
 static void launch_attention(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t sq,
                              int64_t sk, float scale, int causal, hipStream_t stream) {
   const int q_tiles = (int)((sq + BQ - 1) / BQ);
-  dim3 grid((unsigned)(bh * q_tiles)), block(256);
+  dim3 grid((unsigned)(bh * q_tiles)), block(64 * FA_WAVES);
   hipLaunchKernelGGL((attention_fwd<BF, D>), grid, block, 0, stream, (const uint16_t*)q, (const uint16_t*)k,
                      (const uint16_t*)v, (uint16_t*)o, sq, sk, scale, q_tiles, causal);
 }
