@@ -106,6 +106,28 @@ def test_int8_gemm_int32_is_bit_exact(device, m, n, k):
     np.testing.assert_array_equal(c.to_host(), a.astype(np.int64) @ w.astype(np.int64).T)
 
 
+# 33..128 rows with K a whole number of 128-byte slices take the LDS-staged skinny kernel: fewer slices than waves
+# (k=128: one), remainders (3, 5, 7, 9 slices over four waves), ragged rows and columns
+@pytest.mark.parametrize("m,n,k", [(33, 96, 128), (64, 64, 384), (65, 130, 1152), (96, 33, 640), (127, 100, 896),
+                                   (128, 256, 2048)])
+def test_int8_skinny_staged_is_bit_exact(device, m, n, k):
+    rng = np.random.default_rng(5)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    c = device.empty(T.i32, m, n)
+    programs.gemm_i8_i32[programs.Tiling(bm=32, bn=32, bk=32)](device.to_device(a), device.to_device(w), c)
+    np.testing.assert_array_equal(c.to_host(), a.astype(np.int64) @ w.astype(np.int64).T)
+
+
+@pytest.mark.parametrize("m,n,k", [(33, 96, 64), (100, 70, 320), (128, 256, 1088)])
+def test_bf16_skinny_staged_agrees_with_the_float64_bound(device, m, n, k):
+    rng = np.random.default_rng(6)
+    (aw, a), (bw, b) = bf16_normal(rng, (m, k)), bf16_normal(rng, (n, k))
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_nt[programs.Tiling(bm=64, bn=64, bk=32)](device.to_device(aw, T.bf16), device.to_device(bw, T.bf16), c)
+    assert_agrees(bf16_values(c.to_host()), a, b.T, k, "bf16")
+
+
 @pytest.mark.parametrize("m,n,k", [(16, 512, 256), (96, 200, 160), (33, 65, 64)])
 def test_w8a8_dequant_epilogue_is_bit_exact_against_the_oracle(device, m, n, k):
     """int32 accumulation is exact, so the whole result is: bf16(f32(f32(acc) * sa[m]) * sw[n])."""
