@@ -4,9 +4,9 @@
 // `c[rows, cols] = f(acc).to(dtype)` (reference compiler/ir.py:309-315 Accumulate, compiler/emit.py:788-821). One
 // workgroup owns a BM x BN output tile, four waves split it 2 x 2, and every wave keeps its accumulators in
 // registers as 32x32 MFMA blocks. Main loops: `gemm_pipe` (bf16/f16/int8) and `gemm_pp` (fp8) for whole 256 x 256
-// tiles (rings of direct-to-LDS slices, see there), `gemm_skinny` for M <= 32, `gemm_skinny_staged` for M <= 128,
-// and `gemm_tile` for ragged shapes (128-byte slices staged through registers, bounds-checked, double buffered). All end in the same epilogue,
-// `patch_put` + `patch_store`.
+// tiles (rings of direct-to-LDS slices, see there), `gemm_skinny` for M <= 128 (rings of direct-to-LDS slices per
+// wave), and `gemm_tile` for ragged shapes (128-byte slices staged through registers, bounds-checked, double
+// buffered). All end in the same epilogue, `patch_put` + `patch_store`.
 //
 // One byte-oriented main loop serves three operand formats, because each MFMA consumes the same 16 bytes per lane
 // per half-wave:
@@ -713,14 +713,18 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
       store_block<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wr + i * 32, n0 + wc + j * 32, M, N, e, lane);
 }
 
-// Skinny products (M <= 32 here; up to 128 in `gemm_skinny_staged`), the HBM-bound shapes: B (N x K) is streamed once and A is small enough to be served
-// from L2. A workgroup owns 32 output columns and all M rows (MT blocks of 32); its WAVES waves split K, wave w
-// taking one contiguous run of 128-byte K slices (runs far apart in a row keep each wave's HBM requests on few DRAM
-// pages: +25 % over interleaved slices). Operands go straight from global memory into MFMA registers with no LDS staging: lane (r32, half)
-// loads bytes [half * 64, half * 64 + 64) of its row's slice as four 16-byte loads, and MFMA step s takes the s-th
-// 16 bytes of them (32 bytes for fp8). A and B use the same K permutation, so the dot products are unchanged. The
-// partial sums meet in LDS, and waves 0..MT-1 each store one 32 x 32 block through the common epilogue.
-template <int FMT, int MT, int WAVES, int U>
+// Skinny products (M <= 128), the HBM-bound shapes: B (N x K) is streamed from HBM once and A (M x K) is read by
+// every workgroup from L2. A workgroup owns 32 output columns and all M rows (MT blocks of 32); its WAVES waves split
+// K, wave w taking one contiguous run of 128-byte K slices (runs far apart in a row keep each wave's HBM requests on
+// few DRAM pages). Each wave moves its slices of A and B into its own LDS ring with direct-to-LDS loads that cover 8
+// whole 128-byte rows per instruction, then reads the MFMA operands from LDS: loads with one lane per row (32 rows x
+// 16 bytes per instruction) would fetch every line four times. Row R of a staged slice holds its 16-byte chunk c at
+// position c ^ ((R >> 1) & 7), so a ds_read_b128 of one chunk from 16 consecutive rows touches all 64 banks once.
+// Lane (r32, half) takes chunks half * 4 + q of its row for A and for B alike, and MFMA step s the s-th 16 bytes of
+// them (32 bytes for fp8): both operands see the same K permutation, so the dot products are unchanged. The ring has
+// STAGES stages per wave, STAGES - 1 slices in flight while one is multiplied. The partial sums meet in LDS, and
+// waves 0..MT-1 each store one 32 x 32 block through the common epilogue.
+template <int FMT, int MT, int WAVES, int STAGES>
 __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __restrict__ A,
                                                               const uint8_t* __restrict__ B, void* __restrict__ C,
                                                               int64_t M, int64_t N, int64_t kbytes, int64_t lda,
@@ -728,133 +732,32 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __re
   typedef Mfma<FMT> Unit;
   typedef typename Unit::Acc Acc;
   typedef std::conditional_t<FMT == FMT_I8, int, float> Elem;
-  constexpr int CH = Unit::kBytes / 32;  // 16-byte registers per lane per MFMA step
-  constexpr int STEPS = 4 / CH;          // MFMA steps per 128-byte slice
-  constexpr int RED_WORDS = WAVES * MT * 16 * 64;
-  constexpr int LDS_WORDS = RED_WORDS > WAVES * PATCH_WORDS ? RED_WORDS : WAVES * PATCH_WORDS;
-  __shared__ __attribute__((aligned(16))) uint32_t lds[LDS_WORDS];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int half = lane >> 5, r32 = lane & 31;
-  const int64_t n0 = (int64_t)blockIdx.x * 32;
-  // columns past the end read the last one; the epilogue does not store them
-  const uint8_t* bp = B + min(n0 + r32, N - 1) * ldb + half * 64;
-  const uint8_t* ap[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) ap[t] = A + min((int64_t)t * 32 + r32, M - 1) * lda + half * 64;
-  const int nk = (int)(kbytes / 128);
-  Acc acc[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = Acc{};
-  // wave w: the slices [w * per, (w + 1) * per), then slice WAVES * per + w when K does not split evenly
-  const int per = nk / WAVES;
-  for (int first = wave * per; first < (wave + 1) * per; first += U) {
-    u32x4 rb[U][4], ra[U][MT][4];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int slice = first + u;
-      if (slice < (wave + 1) * per) {
-        const int64_t off = (int64_t)slice * 128;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) rb[u][q] = *reinterpret_cast<const u32x4*>(bp + off + q * 16);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          if (t * 32 + r32 < M) {  // rows past the end need no load: their results are never stored
-#pragma unroll
-            for (int q = 0; q < 4; ++q) ra[u][t][q] = *reinterpret_cast<const u32x4*>(ap[t] + off + q * 16);
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) ra[u][t][q] = u32x4{};
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (first + u < (wave + 1) * per) {
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s)
-#pragma unroll
-          for (int t = 0; t < MT; ++t) Unit::step(acc[t], &ra[u][t][s * CH], &rb[u][s * CH]);
-      }
-    }
-  }
-  if (WAVES * per + wave < nk) {
-    u32x4 rb[4], ra[MT][4];
-    const int64_t off = (int64_t)(WAVES * per + wave) * 128;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) rb[q] = *reinterpret_cast<const u32x4*>(bp + off + q * 16);
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        ra[t][q] = t * 32 + r32 < M ? *reinterpret_cast<const u32x4*>(ap[t] + off + q * 16) : u32x4{};
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) Unit::step(acc[t], &ra[t][s * CH], &rb[s * CH]);
-  }
-  Elem* partial = reinterpret_cast<Elem*>(lds);
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) partial[((wave * MT + t) * 16 + r) * 64 + lane] = acc[t][r];
-  __syncthreads();
-  Acc sum = Acc{};
-  if (wave < MT) {
-    for (int v = 0; v < WAVES; ++v)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sum[r] += partial[((v * MT + wave) * 16 + r) * 64 + lane];
-  }
-  __syncthreads();
-  if (wave < MT)
-    store_block<FMT == FMT_I8, true>(sum, lds + wave * PATCH_WORDS, C, ldc, (int64_t)wave * 32, n0, M, N, e, lane);
-}
-
-
-// Skinny products with 33..128 rows. Every workgroup reads all of A (M x K) from L2, so there A's loads set the pace,
-// and the lane-per-row loads of `gemm_skinny` (32 rows x 16 bytes per instruction) fetch each 128-byte line four
-// times. Here each wave moves its K slice of A into its own LDS ring with direct-to-LDS loads that cover 8 whole rows
-// per instruction, then reads the MFMA operands from LDS; B keeps the register loads (one 32-row tile, streamed from
-// HBM once). Row R of a staged 128-byte slice holds its 16-byte chunk c at position c ^ ((R >> 1) & 7), so a
-// ds_read_b128 of one chunk from 16 consecutive rows touches all 64 banks once. The ring has two stages per wave:
-// slice i + 1 (A by DMA, B into registers) is in flight while slice i is multiplied. Waves split K into contiguous
-// runs as in `gemm_skinny`, and the partial sums meet the same way.
-template <int FMT, int MT, int WAVES>
-__global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny_staged(const uint8_t* __restrict__ A,
-                                                                    const uint8_t* __restrict__ B,
-                                                                    void* __restrict__ C, int64_t M, int64_t N,
-                                                                    int64_t kbytes, int64_t lda, int64_t ldb,
-                                                                    int64_t ldc, Epilogue e) {
-  typedef Mfma<FMT> Unit;
-  typedef typename Unit::Acc Acc;
-  typedef std::conditional_t<FMT == FMT_I8, int, float> Elem;
-  constexpr int CH = Unit::kBytes / 32;  // 16-byte registers per lane per MFMA step
-  constexpr int STEPS = 4 / CH;          // MFMA steps per 128-byte slice
-  constexpr int STAGE = MT * 4096;       // one slice of A: MT * 32 rows of 128 bytes
-  constexpr int RING_WORDS = WAVES * 2 * STAGE / 4;
+  constexpr int CH = Unit::kBytes / 32;       // 16-byte registers per lane per MFMA step
+  constexpr int STEPS = 4 / CH;               // MFMA steps per 128-byte slice
+  constexpr int STAGE = (MT + 1) * 4096;      // one slice: MT * 32 rows of A, then 32 rows of B, 128 bytes each
+  constexpr int LOADS = (MT + 1) * 4;         // DMA instructions per slice
+  constexpr int AHEAD = (STAGES - 1) * LOADS; // loads still in flight when the oldest slice is waited for
+  constexpr int RING_WORDS = WAVES * STAGES * STAGE / 4;
   constexpr int RED_WORDS = WAVES * MT * 16 * 64;
   constexpr int W1 = RING_WORDS > RED_WORDS ? RING_WORDS : RED_WORDS;
   constexpr int LDS_WORDS = W1 > WAVES * PATCH_WORDS ? W1 : WAVES * PATCH_WORDS;
-  constexpr int NEXT = MT * 4 + 4;  // loads per slice: MT * 4 DMA instructions for A, 4 for B
+  static_assert(LDS_WORDS * 4 <= 160 * 1024, "the ring exceeds the LDS of a CU");
   __shared__ __attribute__((aligned(16))) uint32_t lds[LDS_WORDS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, r32 = lane & 31;
   const int64_t n0 = (int64_t)blockIdx.x * 32;
-  // columns past the end read the last one; the epilogue does not store them
-  const uint8_t* bp = B + min(n0 + r32, N - 1) * ldb + half * 64;
-  // DMA instruction (t, q) fills rows t * 32 + q * 8 .. + 7 of the stage; lane L lands at position L & 7 of row L >> 3
-  // and so fetches the chunk that the swizzle puts there. Rows past the end read the last row (never stored).
-  const uint8_t* asrc[MT][4];
+  // DMA instruction j fills rows 8 j .. 8 j + 7 of the stage (A's rows first, then B's); lane L lands at position
+  // L & 7 of row 8 j + (L >> 3) and so fetches the chunk that the swizzle puts there. Rows past the end of A or B
+  // read the last row: their results are never stored.
+  const uint8_t* src[LOADS];
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t row = t * 32 + q * 8 + (lane >> 3);
-      const int chunk = (lane & 7) ^ ((q * 4 + (lane >> 4)) & 7);
-      asrc[t][q] = A + min(row, M - 1) * lda + chunk * 16;
-    }
-  uint8_t* ring = reinterpret_cast<uint8_t*>(lds) + wave * 2 * STAGE;
-  // lane (r32, half) takes chunks half * 4 + q of its row, as the B registers do
+  for (int j = 0; j < LOADS; ++j) {
+    const int chunk = (lane & 7) ^ (((j & 3) * 4 + (lane >> 4)) & 7);
+    const int64_t row = j * 8 + (lane >> 3);  // row of the stage
+    src[j] = j < MT * 4 ? A + min(row, M - 1) * lda + chunk * 16
+                        : B + min(n0 + row - MT * 32, N - 1) * ldb + chunk * 16;
+  }
+  uint8_t* ring = reinterpret_cast<uint8_t*>(lds) + wave * STAGES * STAGE;
   int rd[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) rd[q] = r32 * 128 + (((half * 4 + q) ^ ((r32 >> 1) & 7)) * 16);
@@ -864,60 +767,53 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny_staged(const uint8_
   Acc acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = Acc{};
-  auto issue = [&](int slice, int stage, u32x4* rb) {
+  auto issue = [&](int slice, int stage) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of the stage are done before it is refilled
     const int64_t off = (int64_t)slice * 128;
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        __builtin_amdgcn_global_load_lds((const void*)(asrc[t][q] + off),
-                                         (__attribute__((address_space(3))) void*)(ring + stage * STAGE +
-                                                                                   (t * 4 + q) * 1024),
-                                         16, 0, 0);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) rb[q] = *reinterpret_cast<const u32x4*>(bp + off + q * 16);
+    for (int j = 0; j < LOADS; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(src[j] + off),
+                                       (__attribute__((address_space(3))) void*)(ring + stage * STAGE + j * 1024), 16,
+                                       0, 0);
   };
-  auto consume = [&](int stage, const u32x4* rb) {
-    u32x4 ra[MT][4];
+  auto consume = [&](int stage) {
+    const uint8_t* base = ring + stage * STAGE;
+    u32x4 ra[MT][4], rb[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rb[q] = *reinterpret_cast<const u32x4*>(base + MT * 4096 + rd[q]);
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        ra[t][q] = *reinterpret_cast<const u32x4*>(ring + stage * STAGE + t * 4096 + rd[q]);
+      for (int q = 0; q < 4; ++q) ra[t][q] = *reinterpret_cast<const u32x4*>(base + t * 4096 + rd[q]);
 #pragma unroll
     for (int s = 0; s < STEPS; ++s)
 #pragma unroll
       for (int t = 0; t < MT; ++t) Unit::step(acc[t], &ra[t][s * CH], &rb[s * CH]);
   };
-  // vmcnt(NEXT): everything but the newest slice's loads has landed (gfx9 s_waitcnt encoding, other counters free)
-#define KRN_WAIT_ALL_BUT_NEXT __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | (NEXT & 15) | ((NEXT >> 4) << 14))
-#define KRN_WAIT_ALL __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00)
-  // two slices per iteration so that the stage and the B registers are fixed in the steady state (no branches in
-  // it: the waits stay exact)
-  u32x4 rb0[4], rb1[4];
-  if (cnt > 0) issue(begin, 0, rb0);
+#pragma unroll
+  for (int p = 0; p < STAGES - 1; ++p)
+    if (p < cnt) issue(begin + p, p);
+  // steady state: STAGES slices per iteration, so every stage index is a constant and there are no branches (the
+  // waits stay exact); vmcnt(AHEAD) = all but the newest STAGES - 1 slices have landed (gfx9 s_waitcnt encoding,
+  // other counters left free)
   int i = 0;
-  for (; i + 2 < cnt; i += 2) {
-    issue(begin + i + 1, 1, rb1);
-    KRN_WAIT_ALL_BUT_NEXT;
-    consume(0, rb0);
-    issue(begin + i + 2, 0, rb0);
-    KRN_WAIT_ALL_BUT_NEXT;
-    consume(1, rb1);
+  for (; i + 2 * STAGES - 2 < cnt; i += STAGES) {
+#pragma unroll
+    for (int j = 0; j < STAGES; ++j) {
+      issue(begin + i + j + STAGES - 1, (j + STAGES - 1) % STAGES);
+      __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | (AHEAD & 15) | ((AHEAD >> 4) << 14));
+      consume(j);
+    }
   }
-  if (i + 1 < cnt) {
-    issue(begin + i + 1, 1, rb1);
-    KRN_WAIT_ALL_BUT_NEXT;
-    consume(0, rb0);
-    KRN_WAIT_ALL;
-    consume(1, rb1);
-  } else if (i < cnt) {
-    KRN_WAIT_ALL;
-    consume(0, rb0);
+  // at most 2 * STAGES - 2 slices are left, and i is a multiple of STAGES
+#pragma unroll
+  for (int j = 0; j < 2 * STAGES - 2; ++j) {
+    if (i + j < cnt) {
+      if (i + j + STAGES - 1 < cnt) issue(begin + i + j + STAGES - 1, (j + STAGES - 1) % STAGES);
+      __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00);  // vmcnt(0)
+      consume(j % STAGES);
+    }
   }
-#undef KRN_WAIT_ALL_BUT_NEXT
-#undef KRN_WAIT_ALL
   __syncthreads();  // the partial sums overwrite other waves' rings
   Elem* partial = reinterpret_cast<Elem*>(lds);
 #pragma unroll
@@ -1009,15 +905,11 @@ static int launch_pp(const void* a, const void* b, void* c, int64_t m, int64_t n
 template <int FMT, int MT>
 static int launch_skinny_mt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                             int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  // up to 32 rows, operands straight into registers (8 waves of 2-slice batches); past that A through LDS (4 waves:
-  // the two-stage rings of 4 waves fill 128 KiB at 128 rows)
-  if constexpr (MT == 1) {
-    hipLaunchKernelGGL((gemm_skinny<FMT, 1, 8, 2>), dim3((unsigned)((n + 31) / 32)), dim3(8 * 64), 0, stream,
-                       (const uint8_t*)a, (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
-  } else {
-    hipLaunchKernelGGL((gemm_skinny_staged<FMT, MT, 4>), dim3((unsigned)((n + 31) / 32)), dim3(4 * 64), 0, stream,
-                       (const uint8_t*)a, (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
-  }
+  // four waves (one per SIMD, all issuing MFMAs: fewer leave bf16 compute-bound at 128 rows); three stages for one
+  // row block, two above (the ring then takes 96 to 160 KiB)
+  constexpr int STAGES = MT == 1 ? 3 : 2;
+  hipLaunchKernelGGL((gemm_skinny<FMT, MT, 4, STAGES>), dim3((unsigned)((n + 31) / 32)), dim3(4 * 64), 0, stream,
+                     (const uint8_t*)a, (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     krn_set_error("gemm launch: %s", hipGetErrorString(err));
