@@ -40,12 +40,6 @@ struct Epilogue {
   const void* vec[4];    // per-row (length M) or per-column (length N) vectors
 };
 
-__device__ __forceinline__ float vec_at(const void* v, int kind, int64_t i) {
-  if (kind == 1) return h2f(static_cast<const uint16_t*>(v)[i]);
-  if (kind == 2) return bf2f(static_cast<const uint16_t*>(v)[i]);
-  return static_cast<const float*>(v)[i];
-}
-
 __device__ __forceinline__ float activation(int op, float x) {
   if (op == RELU) return x < 0.0f ? 0.0f : x;
   if (op == GELU) return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, erff(__fmul_rn(x, 0.7071067811865476f))));
@@ -124,10 +118,60 @@ __device__ __forceinline__ void patch_put(const V& block, uint32_t* patch, int l
   }
 }
 
-// Memory half: the patch through the epilogue to C.
-template <bool INT>
+// Entry i of a vector of float32 (`kind` 0) or 16-bit values (1 = f16, 2 = bf16) as raw bits, and their value
+__device__ __forceinline__ uint32_t vec_bits(const void* v, int kind, int64_t i) {
+  return kind == 0 ? static_cast<const uint32_t*>(v)[i] : static_cast<const uint16_t*>(v)[i];
+}
+
+__device__ __forceinline__ float bits_value(int kind, uint32_t b) {
+  return kind == 0 ? __uint_as_float(b) : kind == 1 ? h2f((uint16_t)b) : bf2f((uint16_t)b);
+}
+
+// Columns n .. n + 15 from raw bits, zero from N on; one branch on the kind for all 16
+__device__ __forceinline__ void decode16(int kind, const uint32_t* b, int64_t n, int64_t N, float* s) {
+  if (kind == 0) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) s[c] = __uint_as_float(b[c]);
+  } else if (kind == 1) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) s[c] = h2f((uint16_t)b[c]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) s[c] = bf2f((uint16_t)b[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c) s[c] = n + c < N ? s[c] : 0.0f;
+}
+
+// The vector operands of a 32 x 32 block's epilogue, fetched ahead by every lane of the storing wave: for a per-row
+// operation i the entry of the lane's row (row0 + lane / 2, as the memory half stores), for a per-column one the
+// entry of column col0 + lane % 32. Every load is unconditional (a 32-bit and a 16-bit one per operation, the unused
+// ones reading the valid address `dummy`) and only raw bits are kept, so that no branch merge or decode waits on
+// these loads before the epilogue.
+struct EpiPre {
+  uint32_t w32[4], w16[4];
+};
+
+__device__ __forceinline__ void epi_prefetch(EpiPre& p, const Epilogue& e, const void* dummy, int64_t row0,
+                                             int64_t col0, int64_t M, int64_t N, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int op = e.op[i] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[i] >> VEC_KIND_SHIFT;
+    const bool row = i < e.nops && op < RELU && op % 3 == 1, col = i < e.nops && op < RELU && op % 3 == 2;
+    const int64_t at = row ? min(row0 + (lane >> 1), M - 1) : col ? min(col0 + (lane & 31), N - 1) : 0;
+    p.w32[i] = static_cast<const uint32_t*>((row || col) && kind == 0 ? e.vec[i] : dummy)[(row || col) && kind == 0 ? at : 0];
+    p.w16[i] = static_cast<const uint16_t*>((row || col) && kind != 0 ? e.vec[i] : dummy)[(row || col) && kind != 0 ? at : 0];
+  }
+}
+
+// Memory half: the patch through the epilogue to C. ACT = false: the caller has checked that no operation is an
+// activation, and their code (erff, expf and a divide for each of 16 values) stays out. PRE: the vector operands
+// were fetched ahead by `epi_prefetch` (one value per lane and operation) and reach the lanes that need them by
+// cross-lane permutes; the whole wave must then be active.
+template <bool INT, bool ACT = true, bool PRE = false>
 __device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int64_t ldc, int64_t row0, int64_t col0,
-                                                   int64_t M, int64_t N, const Epilogue& e, int lane) {
+                                                   int64_t M, int64_t N, const Epilogue& e, int lane,
+                                                   const EpiPre* pre = nullptr) {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the patch is written before any lane reads it
   __builtin_amdgcn_wave_barrier();
   const int rr = lane >> 1, c0 = (lane & 1) * 16;
@@ -140,9 +184,11 @@ __device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();  // the next block may overwrite the patch
   const int64_t m = row0 + rr, n = col0 + c0;
-  if (m >= M) return;
+  const bool live = m < M;
+  if (!PRE && !live) return;
   const bool whole = n + 16 <= N && (ldc % 8) == 0 && (uintptr_t)C % 16 == 0;
   if (INT && e.out_kind == I32) {
+    if (!live) return;
     int32_t* out = static_cast<int32_t*>(C) + m * ldc + n;
     if (whole && (ldc % 4) == 0) {
 #pragma unroll
@@ -156,24 +202,51 @@ __device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int
   float v[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c) v[c] = INT ? (float)(int32_t)bits[c] : __uint_as_float(bits[c]);
-  for (int i = 0; i < e.nops; ++i) {
-    const int op = e.op[i] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[i] >> VEC_KIND_SHIFT;
+  auto apply = [&](int i, auto row_value, auto col_values) {
+    const int op = e.op[i] & ((1 << VEC_KIND_SHIFT) - 1);
     if (op >= RELU) {
+      if constexpr (ACT) {
 #pragma unroll
-      for (int c = 0; c < 16; ++c) v[c] = activation(op, v[c]);
+        for (int c = 0; c < 16; ++c) v[c] = activation(op, v[c]);
+      }
     } else if (op % 3 == 0) {
 #pragma unroll
       for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], e.scalar[i]) : __fadd_rn(v[c], e.scalar[i]);
     } else if (op % 3 == 1) {
-      const float s = vec_at(e.vec[i], kind, m);
+      const float s = row_value();
 #pragma unroll
       for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], s) : __fadd_rn(v[c], s);
     } else {
+      float s[16];
+      col_values(s);
 #pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const float s = n + c < N ? vec_at(e.vec[i], kind, n + c) : 0.0f;
-        v[c] = op < 3 ? __fmul_rn(v[c], s) : __fadd_rn(v[c], s);
+      for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], s[c]) : __fadd_rn(v[c], s[c]);
+    }
+  };
+  if constexpr (PRE) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < e.nops) {
+        const int kind = e.op[i] >> VEC_KIND_SHIFT;
+        const uint32_t mine = kind == 0 ? pre->w32[i] : pre->w16[i];
+        apply(i, [&] { return bits_value(kind, mine); }, [&](float* s) {
+          uint32_t b[16];  // column n + c was fetched by lane c0 + c; all permutes out before any result is used
+#pragma unroll
+          for (int c = 0; c < 16; ++c) b[c] = (uint32_t)__shfl((int)mine, c0 + c);
+          decode16(kind, b, n, N, s);
+        });
       }
+    }
+    if (!live) return;
+  } else {
+    for (int i = 0; i < e.nops; ++i) {
+      const int kind = e.op[i] >> VEC_KIND_SHIFT;
+      apply(i, [&] { return bits_value(kind, vec_bits(e.vec[i], kind, m)); }, [&](float* s) {
+        uint32_t b[16];  // clamped indices: the 16 loads issue back to back
+#pragma unroll
+        for (int c = 0; c < 16; ++c) b[c] = vec_bits(e.vec[i], kind, min(n + c, N - 1));
+        decode16(kind, b, n, N, s);
+      });
     }
   }
   if (e.out_kind == F32) {
@@ -207,16 +280,14 @@ __device__ __noinline__ void patch_store(uint32_t* patch, void* C, int64_t ldc, 
   patch_store_inline<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
 }
 
-// One accumulator block to C. Tiles with many blocks per wave call the out-of-line store (their loop over blocks
-// must unroll completely); the skinny kernel, with at most four blocks, inlines it.
-template <bool INT, bool INLINE = false, typename V>
+// One accumulator block to C through the out-of-line store: the tiles' loops over their blocks must unroll
+// completely, and an inlined store in each copy would not fit. (The skinny kernel, with at most four blocks and the
+// vectors fetched ahead, inlines the store instead.)
+template <bool INT, typename V>
 __device__ __forceinline__ void store_block(const V& block, uint32_t* patch, void* C, int64_t ldc, int64_t row0,
                                             int64_t col0, int64_t M, int64_t N, const Epilogue& e, int lane) {
   patch_put<INT>(block, patch, lane);
-  if constexpr (INLINE)
-    patch_store_inline<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
-  else
-    patch_store<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
+  patch_store<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
 }
 
 // 16 bytes of row `base` starting at byte `kb`, zero past the row's end or for a row outside the matrix. VEC: the
@@ -724,7 +795,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
 // them (32 bytes for fp8): both operands see the same K permutation, so the dot products are unchanged. The ring has
 // STAGES stages per wave, STAGES - 1 slices in flight while one is multiplied. The partial sums meet in LDS, and
 // waves 0..MT-1 each store one 32 x 32 block through the common epilogue.
-template <int FMT, int MT, int WAVES, int STAGES>
+template <int FMT, int MT, int WAVES, int STAGES, bool ACT>
 __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __restrict__ A,
                                                               const uint8_t* __restrict__ B, void* __restrict__ C,
                                                               int64_t M, int64_t N, int64_t kbytes, int64_t lda,
@@ -764,6 +835,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __re
   const int nk = (int)(kbytes / 128);
   const int per = nk / WAVES, rem = nk % WAVES;
   const int begin = wave * per + min(wave, rem), cnt = per + (wave < rem ? 1 : 0);
+  // the storing waves fetch the epilogue's vector operands now: loads issued at the very end of a workgroup would
+  // wait behind the other workgroups' streams
+  EpiPre pre;
+  if (e.nops > 0) epi_prefetch(pre, e, A, (int64_t)wave * 32, n0, M, N, lane);
   Acc acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = Acc{};
@@ -828,8 +903,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __re
       for (int r = 0; r < 16; ++r) sum[r] += partial[((v * MT + wave) * 16 + r) * 64 + lane];
   }
   __syncthreads();
-  if (wave < MT)
-    store_block<FMT == FMT_I8, true>(sum, lds + wave * PATCH_WORDS, C, ldc, (int64_t)wave * 32, n0, M, N, e, lane);
+  if (wave < MT) {
+    patch_put<FMT == FMT_I8>(sum, lds + wave * PATCH_WORDS, lane);
+    patch_store_inline<FMT == FMT_I8, ACT, true>(lds + wave * PATCH_WORDS, C, ldc, (int64_t)wave * 32, n0, M, N, e,
+                                                 lane, &pre);
+  }
 }
 
 }  // namespace krn
@@ -905,11 +983,21 @@ static int launch_pp(const void* a, const void* b, void* c, int64_t m, int64_t n
 template <int FMT, int MT>
 static int launch_skinny_mt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                             int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  // four waves (one per SIMD, all issuing MFMAs: fewer leave bf16 compute-bound at 128 rows); three stages for one
-  // row block, two above (the ring then takes 96 to 160 KiB)
-  constexpr int STAGES = MT == 1 ? 3 : 2;
-  hipLaunchKernelGGL((gemm_skinny<FMT, MT, 4, STAGES>), dim3((unsigned)((n + 31) / 32)), dim3(4 * 64), 0, stream,
-                     (const uint8_t*)a, (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  // four waves (one per SIMD, all issuing MFMAs: fewer leave bf16 compute-bound at 128 rows) and two stages: the
+  // ring takes 64 KiB for one row block, so two workgroups share a CU and one's reduction and epilogue overlap the
+  // other's stream; 96 to 160 KiB for more rows
+  constexpr int STAGES = 2;
+  // an epilogue without activations gets a kernel without their code (a quarter of the size, and no instruction
+  // cache misses in the epilogue)
+  bool act = false;
+  for (int i = 0; i < e.nops; ++i) act |= (e.op[i] & ((1 << VEC_KIND_SHIFT) - 1)) >= RELU;
+  const dim3 grid((unsigned)((n + 31) / 32)), block(4 * 64);
+  if (act)
+    hipLaunchKernelGGL((gemm_skinny<FMT, MT, 4, STAGES, true>), grid, block, 0, stream, (const uint8_t*)a,
+                       (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  else
+    hipLaunchKernelGGL((gemm_skinny<FMT, MT, 4, STAGES, false>), grid, block, 0, stream, (const uint8_t*)a,
+                       (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     krn_set_error("gemm launch: %s", hipGetErrorString(err));

@@ -128,7 +128,8 @@ def test_bf16_skinny_staged_agrees_with_the_float64_bound(device, m, n, k):
     assert_agrees(bf16_values(c.to_host()), a, b.T, k, "bf16")
 
 
-@pytest.mark.parametrize("m,n,k", [(16, 512, 256), (96, 200, 160), (33, 65, 64)])
+@pytest.mark.parametrize("m,n,k", [(16, 512, 256), (96, 200, 160), (33, 65, 64), (33, 65, 128), (100, 70, 384),
+                                   (128, 200, 256)])
 def test_w8a8_dequant_epilogue_is_bit_exact_against_the_oracle(device, m, n, k):
     """int32 accumulation is exact, so the whole result is: bf16(f32(f32(acc) * sa[m]) * sw[n])."""
     rng = np.random.default_rng(4)

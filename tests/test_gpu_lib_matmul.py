@@ -23,7 +23,9 @@ ACT = {
     "gelu": lambda x: 0.5 * x * (1 + ERF(x / math.sqrt(2))),
     "silu": lambda x: x / (1 + np.exp(-x)),
 }
-SHAPES = [(50, 38, 70), (256, 512, 256), (130, 257, 64)]
+# the last two take the skinny kernel (at most 128 rows, K a whole number of 128-byte slices), whose epilogue fetches
+# the bias ahead and shares it across lanes; ragged N there
+SHAPES = [(50, 38, 70), (256, 512, 256), (130, 257, 64), (100, 130, 64), (7, 45, 192)]
 
 
 def reference(a, b, bias, flags):
