@@ -456,6 +456,17 @@ __global__ __launch_bounds__(256, 1) void gemm_tile(const uint8_t* __restrict__ 
 // at its swizzled slot. Fragments are double-buffered in registers: the LDS reads of step s + 1 (and, at the end of
 // a slice, of the next slice) are issued before the MFMAs of step s, and the scheduler is told to interleave one
 // LDS read or one global load with each MFMA, so the memory instructions issue in the shadow of the matrix core.
+// A buffer resource whose records start at `base` (raw 32-bit offsets up to 2^31 - 1, no stride, no swizzle)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const uint8_t* base) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7fffffff, 0x00020000);
+}
+
+// 16 bytes per lane from resource offset voff + soff straight into LDS: the wave's 64 lanes fill 1 KiB at `dst`
+// (buffer_load_dwordx4 ... lds). A device function so that the host pass never sees the builtin.
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
 template <int BKB>
 __device__ __forceinline__ int swzk(int row) {
   return BKB == 128 ? swz8(row) : swz4(row);
@@ -489,23 +500,26 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   int tm, tn;
   tile_of((int)(M / BM), (int)(N / BN), tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int half = lane >> 5, r32 = lane & 31;
 
-  // this lane's share of each wave load: its row within the 1 KiB block and the global chunk for its slot
+  // this lane's share of each wave load: its row within the 1 KiB block and the global chunk for its slot. Loads go
+  // through buffer resources over this tile's A and B panels (base in SGPRs): a lane keeps one 32-bit panel offset
+  // per load and the slice offset is an SGPR, so no address arithmetic runs per load (the host routes a tile here
+  // only when its panel offsets fit in 31 bits).
   const int lrow = lane / CPR, lslot = lane % CPR;
-  const uint8_t* a_src[LOADS_A];
-  const uint8_t* b_src[LOADS_B];
+  const __amdgpu_buffer_rsrc_t a_rsrc = panel_rsrc(A + m0 * lda), b_rsrc = panel_rsrc(B + n0 * ldb);
+  uint32_t a_off_g[LOADS_A], b_off_g[LOADS_B];
 #pragma unroll
   for (int j = 0; j < LOADS_A; ++j) {
     const int row = (wave * LOADS_A + j) * ROWS_PER_LOAD + lrow;
-    a_src[j] = A + (m0 + row) * lda + (lslot ^ swzk<BKB>(row)) * 16;
+    a_off_g[j] = (uint32_t)(row * lda + (lslot ^ swzk<BKB>(row)) * 16);
   }
 #pragma unroll
   for (int j = 0; j < LOADS_B; ++j) {
     const int row = (wave * LOADS_B + j) * ROWS_PER_LOAD + lrow;
-    b_src[j] = B + (n0 + row) * ldb + (lslot ^ swzk<BKB>(row)) * 16;
+    b_off_g[j] = (uint32_t)(row * ldb + (lslot ^ swzk<BKB>(row)) * 16);
   }
   // fragment offsets (16-byte units within a stage) of every MFMA operand this lane reads
   int a_off[TM][KS][CH], b_off[TN][KS][CH];
@@ -530,13 +544,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
 #define KRN_ISSUE(slice)                                                                                        \
   do {                                                                                                          \
     uint8_t* stage = lds + ((slice) % STAGES) * STAGE_BYTES;                                                    \
-    const int64_t koff = (int64_t)(slice) * BKB;                                                                \
-    _Pragma("unroll") for (int j = 0; j < LOADS_A; ++j) __builtin_amdgcn_global_load_lds(                       \
-        (const void*)(a_src[j] + koff),                                                                         \
-        (__attribute__((address_space(3))) void*)(stage + (wave * LOADS_A + j) * 1024), 16, 0, 0);              \
-    _Pragma("unroll") for (int j = 0; j < LOADS_B; ++j) __builtin_amdgcn_global_load_lds(                       \
-        (const void*)(b_src[j] + koff),                                                                         \
-        (__attribute__((address_space(3))) void*)(stage + BM * BKB + (wave * LOADS_B + j) * 1024), 16, 0, 0);   \
+    const int koff = (slice) * BKB;                                                                             \
+    _Pragma("unroll") for (int j = 0; j < LOADS_A; ++j)                                                         \
+        buffer_to_lds16(a_rsrc, stage + (wave * LOADS_A + j) * 1024, a_off_g[j], koff);                         \
+    _Pragma("unroll") for (int j = 0; j < LOADS_B; ++j)                                                         \
+        buffer_to_lds16(b_rsrc, stage + BM * BKB + (wave * LOADS_B + j) * 1024, b_off_g[j], koff);              \
   } while (0)
   // vmcnt(n) with lgkmcnt and expcnt left alone (gfx9 s_waitcnt encoding), then every LDS read of this wave done
   // and the workgroup barrier
@@ -670,20 +682,21 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
   int tm, tn;
   tile_of((int)(M / BM), (int)(N / BN), tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = wave >> 2, q = wave & 3;
   const int half = lane >> 5, r32 = lane & 31;
 
   // loads: group 0 fills the A part of a stage, group 1 the B part; wave q the rows [64 q, 64 q + 64)
   const int lrow = lane / CPR, lslot = lane % CPR;
-  const uint8_t* src[LOADS];
+  // through a buffer resource over the group's panel, as in gemm_pipe
+  const __amdgpu_buffer_rsrc_t rsrc = panel_rsrc(g ? B + n0 * ldb : A + m0 * lda);
+  uint32_t src_off[LOADS];
   {
-    const uint8_t* base = g ? B + n0 * ldb : A + m0 * lda;
     const int64_t ld = g ? ldb : lda;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int row = (q * LOADS + j) * 16 + lrow;
-      src[j] = base + row * ld + (lslot ^ swz4(row)) * 16;
+      src_off[j] = (uint32_t)(row * ld + (lslot ^ swz4(row)) * 16);
     }
   }
   const int dst0 = g * PART + q * LOADS * 1024;
@@ -711,9 +724,8 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
 #define KRN_ISSUE(slice)                                                                                        \
   do {                                                                                                          \
     uint8_t* stage = lds + ((slice) % STAGES) * STAGE_BYTES + dst0;                                             \
-    const int64_t koff = (int64_t)(slice) * BKB;                                                                \
-    _Pragma("unroll") for (int j = 0; j < LOADS; ++j) __builtin_amdgcn_global_load_lds(                         \
-        (const void*)(src[j] + koff), (__attribute__((address_space(3))) void*)(stage + j * 1024), 16, 0, 0);   \
+    const int koff = (slice) * BKB;                                                                             \
+    _Pragma("unroll") for (int j = 0; j < LOADS; ++j) buffer_to_lds16(rsrc, stage + j * 1024, src_off[j], koff); \
   } while (0)
 #define KRN_VMWAIT(n) __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | ((n) & 15) | (((n) >> 4) << 14))
 #define KRN_LGKWAIT() __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00)
@@ -1044,7 +1056,9 @@ static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t
   const int64_t big = ((m + 255) / 256) * ((n + 255) / 256);
   const bool vec = kbytes % 16 == 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0;
   const bool large = big >= 256 && vec;
-  const bool whole = vec && m % 256 == 0 && n % 256 == 0 && kbytes % 128 == 0 && kbytes > 0 && large;
+  // whole tiles: the 256-row operand panels are addressed by 31-bit buffer offsets
+  const bool whole = vec && m % 256 == 0 && n % 256 == 0 && kbytes % 128 == 0 && kbytes > 0 && large &&
+                     256 * lda <= 0x7fffffff;
   // few rows: stream B once with every CU busy (whole tiles would leave most CUs idle)
   const bool skinny = vec && m > 0 && m <= 128 && n > 0 && kbytes % 128 == 0 && kbytes > 0;
 #define KRN_GEMM(F)                                                                                    \
