@@ -127,20 +127,20 @@ __device__ __forceinline__ float bits_value(int kind, uint32_t b) {
   return kind == 0 ? __uint_as_float(b) : kind == 1 ? h2f((uint16_t)b) : bf2f((uint16_t)b);
 }
 
-// Columns n .. n + 15 from raw bits, zero from N on; one branch on the kind for all 16
-__device__ __forceinline__ void decode16(int kind, const uint32_t* b, int64_t n, int64_t N, float* s) {
+// Columns n .. n + 7 from raw bits, zero from N on; one branch on the kind for all eight
+__device__ __forceinline__ void decode8(int kind, const uint32_t* b, int64_t n, int64_t N, float* s) {
   if (kind == 0) {
 #pragma unroll
-    for (int c = 0; c < 16; ++c) s[c] = __uint_as_float(b[c]);
+    for (int c = 0; c < 8; ++c) s[c] = __uint_as_float(b[c]);
   } else if (kind == 1) {
 #pragma unroll
-    for (int c = 0; c < 16; ++c) s[c] = h2f((uint16_t)b[c]);
+    for (int c = 0; c < 8; ++c) s[c] = h2f((uint16_t)b[c]);
   } else {
 #pragma unroll
-    for (int c = 0; c < 16; ++c) s[c] = bf2f((uint16_t)b[c]);
+    for (int c = 0; c < 8; ++c) s[c] = bf2f((uint16_t)b[c]);
   }
 #pragma unroll
-  for (int c = 0; c < 16; ++c) s[c] = n + c < N ? s[c] : 0.0f;
+  for (int c = 0; c < 8; ++c) s[c] = n + c < N ? s[c] : 0.0f;
 }
 
 // The vector operands of a 32 x 32 block's epilogue, fetched ahead by every lane of the storing wave: for a per-row
@@ -217,10 +217,14 @@ __device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int
 #pragma unroll
       for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], s) : __fadd_rn(v[c], s);
     } else {
-      float s[16];
-      col_values(s);
 #pragma unroll
-      for (int c = 0; c < 16; ++c) v[c] = op < 3 ? __fmul_rn(v[c], s[c]) : __fadd_rn(v[c], s[c]);
+      for (int h = 0; h < 2; ++h) {  // eight columns at a time keeps the store's register use small
+        float s[8];
+        col_values(s, h * 8);
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          v[h * 8 + c] = op < 3 ? __fmul_rn(v[h * 8 + c], s[c]) : __fadd_rn(v[h * 8 + c], s[c]);
+      }
     }
   };
   if constexpr (PRE) {
@@ -229,11 +233,11 @@ __device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int
       if (i < e.nops) {
         const int kind = e.op[i] >> VEC_KIND_SHIFT;
         const uint32_t mine = kind == 0 ? pre->w32[i] : pre->w16[i];
-        apply(i, [&] { return bits_value(kind, mine); }, [&](float* s) {
-          uint32_t b[16];  // column n + c was fetched by lane c0 + c; all permutes out before any result is used
+        apply(i, [&] { return bits_value(kind, mine); }, [&](float* s, int c8) {
+          uint32_t b[8];  // column n + c was fetched by lane c0 + c; all permutes out before any result is used
 #pragma unroll
-          for (int c = 0; c < 16; ++c) b[c] = (uint32_t)__shfl((int)mine, c0 + c);
-          decode16(kind, b, n, N, s);
+          for (int c = 0; c < 8; ++c) b[c] = (uint32_t)__shfl((int)mine, c0 + c8 + c);
+          decode8(kind, b, n + c8, N, s);
         });
       }
     }
@@ -241,11 +245,11 @@ __device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int
   } else {
     for (int i = 0; i < e.nops; ++i) {
       const int kind = e.op[i] >> VEC_KIND_SHIFT;
-      apply(i, [&] { return bits_value(kind, vec_bits(e.vec[i], kind, m)); }, [&](float* s) {
-        uint32_t b[16];  // clamped indices: the 16 loads issue back to back
+      apply(i, [&] { return bits_value(kind, vec_bits(e.vec[i], kind, m)); }, [&](float* s, int c8) {
+        uint32_t b[8];  // clamped indices: the loads issue back to back
 #pragma unroll
-        for (int c = 0; c < 16; ++c) b[c] = vec_bits(e.vec[i], kind, min(n + c, N - 1));
-        decode16(kind, b, n, N, s);
+        for (int c = 0; c < 8; ++c) b[c] = vec_bits(e.vec[i], kind, min(n + c8 + c, N - 1));
+        decode8(kind, b, n + c8, N, s);
       });
     }
   }
