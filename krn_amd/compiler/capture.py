@@ -61,6 +61,15 @@ class CaptureError(ValueError):
     """A kernel body outside the captured subset, or a type error in it, at a line of the user's file."""
 
 
+class TargetError(CaptureError):
+    """An unavailable target feature, with the alternative to use (reference compiler/errors.py:56-62)."""
+
+    def __init__(self, feature: str, target: str, reason: str, instead: str) -> None:
+        self.feature, self.target, self.reason, self.instead = feature, target, reason, instead
+        super().__init__(f"{feature} is not available on {target}: {reason.rstrip('.')}. "
+                         f"Instead: {instead.rstrip('.')}.")
+
+
 TENSOR_RANKS = {"Matrix": 2, "Vector": 1, "Tensor3": 3}
 ARITHMETIC = {"add": Op.ADD, "sub": Op.SUB, "mul": Op.MUL, "div": Op.DIV, "truediv": Op.DIV}
 UNARY_MATH = {

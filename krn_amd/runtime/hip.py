@@ -12,7 +12,9 @@ import asyncio
 import ctypes
 import hashlib
 import inspect
+import os
 import threading
+import weakref
 from collections.abc import Callable, Sequence
 from ctypes import c_float, c_int, c_int64, c_void_p
 from dataclasses import is_dataclass
@@ -23,7 +25,7 @@ import numpy as np
 from krn_amd import dtypes as D
 from krn_amd.compiler import cdna4, hipgen, space
 from krn_amd.compiler import ir
-from krn_amd.compiler.capture import capture
+from krn_amd.compiler.capture import TargetError, capture
 from krn_amd.dtypes import BF16, F32, Dtype
 from krn_amd.frontend import Blocks, Kernel, Tensor, const_fields
 from krn_amd.runtime import api, hipapi, library
@@ -402,19 +404,74 @@ class HIPBound(Bound):
 
 
 class HIPGraph(Graph):
-    """Recorded launches replayed in order by one call. The launches are re-issued from their prebound form."""
+    """The launches of one function captured from a stream into a hipGraph and replayed with one hipGraphLaunch
+    (reference runtime/cuda_backend.py:486-551, `CUDAGraph`). A replay needs the recorded arguments (the same
+    objects): the recorded nodes keep their pointers, so new arguments raise TargetError; tensor contents may change
+    between replays. Scratch memory that a recorded launch allocated lives as long as the graph. With
+    KRN_GRAPHS=0 the function is instead called again on every replay (plain launches)."""
 
     def __init__(self, device: "HIPDevice", fn: Callable, args: tuple, kwargs: dict) -> None:
-        self.device, self.fn = device, fn
-        self.args, self.kwargs = args, kwargs
-        fn(*args, **kwargs)
+        self.device, self._fn, self._recorded = device, fn, (args, kwargs)
+        self._executable: int | None = None
+        self._keep: list[tuple[object, ...]] = []
+        if os.environ.get("KRN_GRAPHS", "1") != "0":
+            self._executable = self._capture(*args, **kwargs)
 
     def __call__(self, *args, **kwargs) -> None:
-        self.fn(*(args or self.args), **(kwargs or self.kwargs))
+        recorded_args, recorded_kwargs = self._recorded
+        same = (len(args) == len(recorded_args) and all(a is b for a, b in zip(args, recorded_args))
+                and kwargs.keys() == recorded_kwargs.keys()
+                and all(kwargs[name] is recorded_kwargs[name] for name in kwargs))
+        if self._executable is not None and same:
+            stream = self.device.launch_stream()
+            hipapi.api().hipGraphLaunch(c_void_p(self._executable), c_void_p(stream.handle))
+            stream.note("graph", (self,))
+            return
+        if self._executable is not None:
+            raise TargetError("graph replay", self.device.arch,
+                              "hipGraph nodes keep their recorded arguments; krn does not patch node parameters",
+                              "record a new graph for these arguments or set KRN_GRAPHS=0")
+        self._fn(*args, **kwargs)
 
     def submit(self, *args, **kwargs) -> HIPEvent:
         self(*args, **kwargs)
         return self.device.launch_stream().record()
+
+    def _capture(self, *args, **kwargs) -> int:
+        stream = self.device.capture_stream()
+        handle = c_void_p(stream.handle)
+        hipapi.api().hipStreamBeginCapture(handle, hipapi.CAPTURE_RELAXED)
+        graph = c_void_p()
+        try:
+            with stream:
+                self._fn(*args, **kwargs)
+        except BaseException:  # end the capture and drop its graph, then report the original error
+            if hipapi.api().raw("hipStreamEndCapture", handle, ctypes.byref(graph)) == 0 and graph.value:
+                hipapi.api().raw("hipGraphDestroy", graph)
+            stream._pending.clear()
+            stream._keep.clear()
+            raise
+        hipapi.api().hipStreamEndCapture(handle, ctypes.byref(graph))
+        executable = c_void_p()
+        try:
+            hipapi.api().hipGraphInstantiate(ctypes.byref(executable), graph, None, None, 0)
+        except BaseException:
+            hipapi.api().raw("hipGraphDestroy", graph)
+            raise
+        # what the recorded launches hold (scratch tensors, arguments) now lives with the graph
+        self._keep = list(stream._keep)
+        stream._pending.clear()
+        stream._keep.clear()
+        weakref.finalize(self, _release_graph, executable.value, graph.value)
+        return executable.value
+
+
+def _release_graph(executable: int, graph: int) -> None:
+    try:
+        hipapi.api().raw("hipGraphExecDestroy", c_void_p(executable))
+        hipapi.api().raw("hipGraphDestroy", c_void_p(graph))
+    except Exception:
+        pass
 
 
 class HIPDevice(Device):
@@ -441,6 +498,12 @@ class HIPDevice(Device):
         created = HIPStream(self, hipapi.stream_create())
         self._streams.append(created)
         return created
+
+    def capture_stream(self) -> HIPStream:
+        """The stream graphs are recorded on (one per device, reused)."""
+        if getattr(self, "_capture", None) is None:
+            self._capture = self.stream()
+        return self._capture
 
     def empty(self, dtype, *shape: int) -> HIPTensor:
         element = D.of(dtype)

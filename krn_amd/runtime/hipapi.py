@@ -23,6 +23,9 @@ class HIPError(RuntimeError):
         super().__init__(f"{function} failed with {name} ({code}): {message}")
 
 
+CAPTURE_RELAXED = 2  # hipStreamCaptureModeRelaxed: allocation calls stay legal while a stream records
+
+
 class _Api:
     """The resolved entry points of libamdhip64; built once on first use."""
 
@@ -65,6 +68,12 @@ class _Api:
             ],
             "hipFuncSetAttribute": [c_void_p, c_int, c_int],
             "hipGetLastError": [],
+            "hipStreamBeginCapture": [hipStream_t, c_int],
+            "hipStreamEndCapture": [hipStream_t, POINTER(c_void_p)],
+            "hipGraphInstantiate": [POINTER(c_void_p), c_void_p, c_void_p, c_char_p, c_size_t],
+            "hipGraphLaunch": [c_void_p, hipStream_t],
+            "hipGraphExecDestroy": [c_void_p],
+            "hipGraphDestroy": [c_void_p],
         }  # fmt: skip
         for name, argtypes in signatures.items():
             function = getattr(lib, name)
@@ -75,6 +84,10 @@ class _Api:
             error = self.lib.hipGetErrorName(code).decode()
             message = self.lib.hipGetErrorString(code).decode()
             raise HIPError(name, code, error, message)
+
+    def raw(self, name: str, *args) -> int:
+        """Call a HIP function and return its status instead of raising (clean-up paths)."""
+        return getattr(self.lib, name)(*args)
 
     def __getattr__(self, name: str):  # only called for names not set in __init__: the HIP functions
         function = getattr(self.lib, name)
