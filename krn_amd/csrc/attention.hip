@@ -137,10 +137,12 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
   // the row maximum of half h + 1. So the K tile of the next half is read before this tile's V: tile iteration t
   // reads K(t) and K(t + 1), and V(t). It loads K(t + 2) into the slot K(t - 1) left and V(t + 1) into the slot
   // V(t - 1) left; one barrier per tile publishes both.
-  // Direct-to-LDS loads: lane -> (row within its 1 KiB block, slot).
+  // Direct-to-LDS loads through buffer resources over this head's K and V (base in SGPRs; the host keeps a head's
+  // rows under 2^31 bytes): lane -> (row within its 1 KiB block, slot).
   // Each lane's element offsets inside a tile are fixed: computed once here; a load adds the tile's base (uniform)
   const int lrow = lane / DCH, lslot = lane % DCH;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const __amdgpu_buffer_rsrc_t k_rsrc = panel_rsrc(k), v_rsrc = panel_rsrc(v);
   uint32_t koff[LOADS], voff[LOADS];  // byte offsets within a tile
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
@@ -148,21 +150,19 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
     koff[j] = (uint32_t)(row * D + k_slot<D>(row, lslot) * 8) * 2;
     voff[j] = (uint32_t)(row * D + v_slot<D>(row, lslot) * 8) * 2;
   }
-#define KRN_FA_LOAD(src, tile, base, OFF)                                                                     \
+#define KRN_FA_LOAD(rsrc, tile, base, OFF)                                                                    \
   do {                                                                                                        \
     const int64_t t0 = (int64_t)(tile) * BKEY;                                                                \
     if (t0 + BKEY <= sk) {                                                                                    \
-      const uint8_t* tb = reinterpret_cast<const uint8_t*>((src) + t0 * D);                                   \
-      _Pragma("unroll") for (int j = 0; j < LOADS; ++j) __builtin_amdgcn_global_load_lds(                     \
-          (const void*)(tb + OFF[j]),                                                                         \
-          (__attribute__((address_space(3))) void*)(lds + (base) + (wave_s * LOADS + j) * 1024), 16, 0, 0);   \
+      const int soff = (int)(t0 * D * 2);                                                                     \
+      _Pragma("unroll") for (int j = 0; j < LOADS; ++j)                                                       \
+          buffer_to_lds16(rsrc, lds + (base) + (wave_s * LOADS + j) * 1024, OFF[j], soff);                    \
     } else { /* the ragged last tile: rows past the sequence read the last row (masked, so their p is 0) */   \
       _Pragma("unroll") for (int j = 0; j < LOADS; ++j) {                                                     \
         const int row = (wave * LOADS + j) * ROWS_PER_LOAD + lrow;                                            \
         const int64_t key = min(t0 + row, sk - 1);                                                            \
-        __builtin_amdgcn_global_load_lds(                                                                     \
-            (const void*)(reinterpret_cast<const uint8_t*>((src) + key * D) + (OFF[j] - row * D * 2)),                                              \
-            (__attribute__((address_space(3))) void*)(lds + (base) + (wave_s * LOADS + j) * 1024), 16, 0, 0); \
+        buffer_to_lds16(rsrc, lds + (base) + (wave_s * LOADS + j) * 1024,                                     \
+                        (uint32_t)(key * D * 2) + (OFF[j] - (uint32_t)(row * D * 2)), 0);                     \
       }                                                                                                       \
     }                                                                                                         \
   } while (0)
@@ -234,9 +234,9 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
   f32x16 sa, sb;
   float tmax_next = -INFINITY;  // the scaled row maximum of the next half's raw scores
   if (ntiles > 0) {
-    KRN_FA_LOAD(k, 0, 0, koff);
-    KRN_FA_LOAD(v, 0, V_BASE, voff);
-    if (ntiles > 1) KRN_FA_LOAD(k, 1, TILE_BYTES, koff);
+    KRN_FA_LOAD(k_rsrc, 0, 0, koff);
+    KRN_FA_LOAD(v_rsrc, 0, V_BASE, voff);
+    if (ntiles > 1) KRN_FA_LOAD(k_rsrc, 1, TILE_BYTES, koff);
     KRN_FA_PUBLISH();
     KRN_FA_SCORES(sa, 0, 0);  // the first half is active for every wave
     KRN_FA_RAWMAX(sa, tmax_next);
@@ -299,8 +299,8 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
   for (int t = 0; t < ntiles; ++t) {
     const int knext = kcur == 2 * TILE_BYTES ? 0 : kcur + TILE_BYTES;
     const int kfree = knext == 2 * TILE_BYTES ? 0 : knext + TILE_BYTES;
-    if (t + 2 < ntiles) KRN_FA_LOAD(k, t + 2, kfree, koff);
-    if (t + 1 < ntiles) KRN_FA_LOAD(v, t + 1, V_BASE + ((t + 1) & 1) * TILE_BYTES, voff);
+    if (t + 2 < ntiles) KRN_FA_LOAD(k_rsrc, t + 2, kfree, koff);
+    if (t + 1 < ntiles) KRN_FA_LOAD(v_rsrc, t + 1, V_BASE + ((t + 1) & 1) * TILE_BYTES, voff);
     KRN_FA_HALF(t, 0, sa, sb, kcur, knext);
     KRN_FA_HALF(t, 1, sb, sa, kcur, knext);
     KRN_FA_PUBLISH();
@@ -372,6 +372,10 @@ extern "C" int krn_attention_fwd(int kind, const void* q, const void* k, const v
   if (sk == 0) {
     // no keys: the tile program divides 0 by 0
     krn_set_error("attention: an empty key sequence has no softmax");
+    return -1;
+  }
+  if (sk * d * 2 > 0x7fffffff) {  // K and V tiles are addressed by 31-bit offsets within a head
+    krn_set_error("attention: %lld keys of %lld elements exceed 2 GiB per head", (long long)sk, (long long)d);
     return -1;
   }
   hipStream_t s = (hipStream_t)stream;

@@ -34,6 +34,17 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
+// A buffer resource whose records start at `base` (raw 32-bit offsets up to 2^31 - 1, no stride, no swizzle)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+// 16 bytes per lane from resource offset voff + soff straight into LDS: the wave's 64 lanes fill 1 KiB at `dst`
+// (buffer_load_dwordx4 ... lds). A device function so that the host pass never sees the builtin.
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
 }  // namespace krn
 
 // Host side: the last error message of the calling thread, read through krn_amd_last_error().

@@ -460,17 +460,6 @@ __global__ __launch_bounds__(256, 1) void gemm_tile(const uint8_t* __restrict__ 
 // at its swizzled slot. Fragments are double-buffered in registers: the LDS reads of step s + 1 (and, at the end of
 // a slice, of the next slice) are issued before the MFMAs of step s, and the scheduler is told to interleave one
 // LDS read or one global load with each MFMA, so the memory instructions issue in the shadow of the matrix core.
-// A buffer resource whose records start at `base` (raw 32-bit offsets up to 2^31 - 1, no stride, no swizzle)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const uint8_t* base) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, 0x7fffffff, 0x00020000);
-}
-
-// 16 bytes per lane from resource offset voff + soff straight into LDS: the wave's 64 lanes fill 1 KiB at `dst`
-// (buffer_load_dwordx4 ... lds). A device function so that the host pass never sees the builtin.
-__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
-}
-
 template <int BKB>
 __device__ __forceinline__ int swzk(int row) {
   return BKB == 128 ? swz8(row) : swz4(row);
