@@ -34,9 +34,12 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
-// A buffer resource whose records start at `base` (raw 32-bit offsets up to 2^31 - 1, no stride, no swizzle)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+// A buffer resource over `bytes` bytes from `base` (raw 32-bit offsets, no stride, no swizzle; at most 2^31 - 1).
+// Loads past the end return zeros instead of touching memory: that is how the whole-tile GEMMs read the ragged
+// last rows of an operand.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const void* base, int64_t bytes = 0x7fffffff) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)min(bytes, (int64_t)0x7fffffff),
+                                           0x00020000);
 }
 
 // 16 bytes per lane from resource offset voff + soff straight into LDS: the wave's 64 lanes fill 1 KiB at `dst`

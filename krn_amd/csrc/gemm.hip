@@ -451,8 +451,8 @@ __global__ __launch_bounds__(256, 1) void gemm_tile(const uint8_t* __restrict__ 
                                  n0 + wn * (BN / WN) + j * 32, M, N, e, lane);
 }
 
-// The pipelined main loop for whole tiles (M % BM == N % BN == 0, K a multiple of the BKB-byte slice, rows 16-byte
-// aligned). Operand slices go straight from global memory into LDS (global_load_lds_dwordx4, no register staging)
+// The pipelined main loop for 256 x 256 tiles (the last row and column of tiles may be ragged; K a multiple of the
+// BKB-byte slice, rows 16-byte aligned). Operand slices go straight from global memory into LDS (global_load_lds_dwordx4, no register staging)
 // through a ring of STAGES buffers, so the loads of slice k + STAGES - 1 are in flight while slice k multiplies.
 // One barrier per slice publishes the landed slice and frees the oldest buffer; it is a bare s_barrier, because the
 // workgroup fence of __syncthreads() would wait for every outstanding load and drain the ring. A wave's load
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * STAGE_BYTES];
 
   int tm, tn;
-  tile_of((int)(M / BM), (int)(N / BN), tm, tn);
+  tile_of((int)((M + BM - 1) / BM), (int)((N + BN - 1) / BN), tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -500,9 +500,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   // this lane's share of each wave load: its row within the 1 KiB block and the global chunk for its slot. Loads go
   // through buffer resources over this tile's A and B panels (base in SGPRs): a lane keeps one 32-bit panel offset
   // per load and the slice offset is an SGPR, so no address arithmetic runs per load (the host routes a tile here
-  // only when its panel offsets fit in 31 bits).
+  // only when its panel offsets fit in 31 bits). A panel's resource ends at the operand's last row: rows of a
+  // ragged last tile past it load zeros, and their results are never stored.
   const int lrow = lane / CPR, lslot = lane % CPR;
-  const __amdgpu_buffer_rsrc_t a_rsrc = panel_rsrc(A + m0 * lda), b_rsrc = panel_rsrc(B + n0 * ldb);
+  const __amdgpu_buffer_rsrc_t a_rsrc = panel_rsrc(A + m0 * lda, (M - m0) * lda),
+                              b_rsrc = panel_rsrc(B + n0 * ldb, (N - n0) * ldb);
   uint32_t a_off_g[LOADS_A], b_off_g[LOADS_B];
 #pragma unroll
   for (int j = 0; j < LOADS_A; ++j) {
@@ -673,7 +675,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
   __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * STAGE_BYTES];
 
   int tm, tn;
-  tile_of((int)(M / BM), (int)(N / BN), tm, tn);
+  tile_of((int)((M + BM - 1) / BM), (int)((N + BN - 1) / BN), tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = wave >> 2, q = wave & 3;
@@ -682,7 +684,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
   // loads: group 0 fills the A part of a stage, group 1 the B part; wave q the rows [64 q, 64 q + 64)
   const int lrow = lane / CPR, lslot = lane % CPR;
   // through a buffer resource over the group's panel, as in gemm_pipe
-  const __amdgpu_buffer_rsrc_t rsrc = panel_rsrc(g ? B + n0 * ldb : A + m0 * lda);
+  const __amdgpu_buffer_rsrc_t rsrc = g ? panel_rsrc(B + n0 * ldb, (N - n0) * ldb) : panel_rsrc(A + m0 * lda, (M - m0) * lda);
   uint32_t src_off[LOADS];
   {
     const int64_t ld = g ? ldb : lda;
@@ -952,7 +954,7 @@ static int launch_gemm(const void* a, const void* b, void* c, int64_t m, int64_t
 template <int FMT, int BM, int BN, int WM, int WN, int STAGES, int BKB>
 static int launch_pipe(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                        int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  const int64_t tiles = (m / BM) * (n / BN);
+  const int64_t tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
   if (tiles > 0x7fffffff) {
     krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
     return -1;
@@ -970,7 +972,7 @@ static int launch_pipe(const void* a, const void* b, void* c, int64_t m, int64_t
 template <int FMT, int STAGES>
 static int launch_pp(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                      int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  const int64_t tiles = (m / 256) * (n / 256);
+  const int64_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
   if (tiles > 0x7fffffff) {
     krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
     return -1;
@@ -1025,8 +1027,9 @@ static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64
   return -1;
 }
 
-// Whole 256 x 256 tiles: for bf16/f16 a ring of four 64-byte K slices (two MFMA steps each); for fp8 the ping-pong
-// ring of four 64-byte slices (one MFMA step each); for int8 two 128-byte slices (four MFMA steps each).
+// 256 x 256 tiles (ragged at the edges): for bf16/f16 a ring of four 64-byte K slices (two MFMA steps each); for fp8
+// the ping-pong ring of four 64-byte slices (one MFMA step each); for int8 two 128-byte slices (four MFMA steps
+// each).
 template <int FMT>
 static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
@@ -1049,9 +1052,9 @@ static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t
   const int64_t big = ((m + 255) / 256) * ((n + 255) / 256);
   const bool vec = kbytes % 16 == 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0;
   const bool large = big >= 256 && vec;
-  // whole tiles: the 256-row operand panels are addressed by 31-bit buffer offsets
-  const bool whole = vec && m % 256 == 0 && n % 256 == 0 && kbytes % 128 == 0 && kbytes > 0 && large &&
-                     256 * lda <= 0x7fffffff;
+  // the pipelined 256 x 256 tiles (ragged M and N too): K in whole 128-byte slices, the 256-row operand panels
+  // addressed by 31-bit buffer offsets
+  const bool whole = vec && kbytes % 128 == 0 && kbytes > 0 && large && 256 * lda <= 0x7fffffff;
   // few rows: stream B once with every CU busy (whole tiles would leave most CUs idle)
   const bool skinny = vec && m > 0 && m <= 128 && n > 0 && kbytes % 128 == 0 && kbytes > 0;
 #define KRN_GEMM(F)                                                                                    \

@@ -6,7 +6,7 @@ import pytest
 
 from krn_amd import T
 from oracle import cbackend, emulate
-from oracle.numerics import bf16_values, e4m3_decode, e4m3_encode
+from oracle.numerics import bf16_values, bf16_words, e4m3_decode, e4m3_encode
 from tests.conftest import KERNELS
 from tests.helpers import assert_agrees, bf16_normal
 from tests.kernels import tile_programs as programs
@@ -126,6 +126,51 @@ def test_bf16_skinny_staged_agrees_with_the_float64_bound(device, m, n, k):
     c = device.empty(T.bf16, m, n)
     programs.gemm_nt[programs.Tiling(bm=64, bn=64, bk=32)](device.to_device(aw, T.bf16), device.to_device(bw, T.bf16), c)
     assert_agrees(bf16_values(c.to_host()), a, b.T, k, "bf16")
+
+
+# At least 256 tiles of 256 x 256 with ragged M and N take the pipelined whole-tile kernels: the rows past the end of
+# A and B load zeros through the buffer resources' bounds and the epilogue stores only the inside
+RAGGED = [(4000, 4100, 256), (4097, 3969, 128), (3841, 4351, 384)]
+
+
+@pytest.mark.parametrize("m,n,k", RAGGED)
+def test_bf16_ragged_whole_tiles_agree_with_the_float64_bound(device, m, n, k):
+    rng = np.random.default_rng(7)
+    (aw, a), (bw, b) = bf16_normal(rng, (m, k)), bf16_normal(rng, (n, k))
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_nt[programs.Tiling(bm=64, bn=64, bk=32)](device.to_device(aw, T.bf16), device.to_device(bw, T.bf16), c)
+    assert_agrees(bf16_values(c.to_host()), a, b.T, k, "bf16")
+
+
+@pytest.mark.parametrize("m,n,k", RAGGED)
+def test_w8a8_ragged_whole_tiles_are_bit_exact(device, m, n, k):
+    """int32 accumulation is exact (float64 holds it), so the result is bf16(f32(f32(acc) * sa[m]) * sw[n])."""
+    rng = np.random.default_rng(8)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    sa = (rng.uniform(0.5, 1.5, (m, 1)) / 127).astype(np.float32)
+    sw = (rng.uniform(0.5, 1.5, (1, n)) / 127).astype(np.float32)
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_w8a8[programs.Tiling(bm=32, bn=32, bk=32)](device.to_device(a), device.to_device(w),
+                                                           device.to_device(sa), device.to_device(sw), c)
+    acc = (a.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+    want = bf16_words((acc * sa).astype(np.float32) * sw)
+    np.testing.assert_array_equal(c.to_host(), want)
+
+
+@pytest.mark.parametrize("m,n,k", RAGGED[:2])
+def test_fp8_ragged_whole_tiles_with_per_tensor_scales(device, m, n, k):
+    rng = np.random.default_rng(9)
+    a, b, sa, sb = fp8_operands(rng, m, n, k)
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_fp8[programs.Tiling(bm=64, bn=64, bk=64)](
+        device.to_device(a, T.f8e4m3fn), device.to_device(b, T.f8e4m3fn), c, sa, sb)
+    got = bf16_values(c.to_host()).astype(np.float64)
+    da, db = e4m3_decode(a).astype(np.float64), e4m3_decode(b).astype(np.float64)
+    scale = np.float64(np.float32(sa * sb))
+    reference = (da @ db.T) * scale
+    bound = (8 * 2.0**-24 * (k + 8) * (np.abs(da) @ np.abs(db).T)) * scale + np.abs(reference) * 2.0**-8 * 1.01
+    assert np.all(np.abs(got - reference) <= bound + 1e-30)
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 512, 256), (96, 200, 160), (33, 65, 64), (33, 65, 128), (100, 70, 384),
