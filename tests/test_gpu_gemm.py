@@ -133,6 +133,44 @@ def test_bf16_skinny_staged_agrees_with_the_float64_bound(device, m, n, k):
 RAGGED = [(4000, 4100, 256), (4097, 3969, 128), (3841, 4351, 384)]
 
 
+# Up to 256 tiles of 128 x 128 (and more than 128 rows) take the pipelined loop on 128 x 128 tiles
+MID = [(1000, 1100, 256), (512, 2048, 384), (1500, 2000, 128)]
+
+
+@pytest.mark.parametrize("m,n,k", MID)
+def test_bf16_mid_size_agrees_with_the_float64_bound(device, m, n, k):
+    rng = np.random.default_rng(10)
+    (aw, a), (bw, b) = bf16_normal(rng, (m, k)), bf16_normal(rng, (n, k))
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_nt[programs.Tiling(bm=64, bn=64, bk=32)](device.to_device(aw, T.bf16), device.to_device(bw, T.bf16), c)
+    assert_agrees(bf16_values(c.to_host()), a, b.T, k, "bf16")
+
+
+@pytest.mark.parametrize("m,n,k", MID)
+def test_int8_mid_size_is_bit_exact(device, m, n, k):
+    rng = np.random.default_rng(11)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    c = device.empty(T.i32, m, n)
+    programs.gemm_i8_i32[programs.Tiling(bm=32, bn=32, bk=32)](device.to_device(a), device.to_device(w), c)
+    np.testing.assert_array_equal(c.to_host(), (a.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64))
+
+
+@pytest.mark.parametrize("m,n,k", MID[:2])
+def test_fp8_mid_size_with_per_tensor_scales(device, m, n, k):
+    rng = np.random.default_rng(12)
+    a, b, sa, sb = fp8_operands(rng, m, n, k)
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_fp8[programs.Tiling(bm=64, bn=64, bk=64)](
+        device.to_device(a, T.f8e4m3fn), device.to_device(b, T.f8e4m3fn), c, sa, sb)
+    got = bf16_values(c.to_host()).astype(np.float64)
+    da, db = e4m3_decode(a).astype(np.float64), e4m3_decode(b).astype(np.float64)
+    scale = np.float64(np.float32(sa * sb))
+    reference = (da @ db.T) * scale
+    bound = (8 * 2.0**-24 * (k + 8) * (np.abs(da) @ np.abs(db).T)) * scale + np.abs(reference) * 2.0**-8 * 1.01
+    assert np.all(np.abs(got - reference) <= bound + 1e-30)
+
+
 @pytest.mark.parametrize("m,n,k", RAGGED)
 def test_bf16_ragged_whole_tiles_agree_with_the_float64_bound(device, m, n, k):
     rng = np.random.default_rng(7)
