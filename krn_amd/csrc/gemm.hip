@@ -1045,8 +1045,7 @@ static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_
 }
 
 // Up to one wave of 128 x 128 tiles (at most 256 tiles): the pipelined loop on 128 x 128 tiles with four waves, a
-// 64 KiB ring (measured 20-40 % faster than the register-staged tiles at 1024^3 and 2048^3 for every format; past
-// one wave of tiles the staged kernel, which shares a CU between workgroups, is as fast or faster)
+// 64 KiB ring (measured 20-40 % faster than the register-staged tiles at 1024^3 and 2048^3 for every format)
 template <int FMT>
 static int launch_mid(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                       int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
@@ -1056,25 +1055,45 @@ static int launch_mid(const void* a, const void* b, void* c, int64_t m, int64_t 
     return launch_pipe<FMT, 128, 128, 2, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
 }
 
+// 128 x 256 tiles, eight waves (64 x 64 each), for the products between one wave of 128 x 128 tiles and 128 tiles
+// of 256 x 256 (bf16/f16 and int8)
+template <int FMT>
+static int launch_band(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                       int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+  if constexpr (FMT == FMT_BF16 || FMT == FMT_F16)
+    return launch_pipe<FMT, 128, 256, 2, 4, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  else if constexpr (FMT == FMT_I8)
+    return launch_pipe<FMT, 128, 256, 2, 4, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  else
+    return launch_gemm<FMT, 128, 128, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+}
+
 static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
                          int64_t elem, const Epilogue& e, hipStream_t stream) {
   const int64_t kbytes = k * elem, lda = k * elem, ldb = k * elem;
   const int64_t ldc = n;
-  // Tile selection for 256 CUs: a 256x256 tile when that still gives every CU a tile, else 128x128.
-  const int64_t big = ((m + 255) / 256) * ((n + 255) / 256);
+  // Kernel choice on 256 CUs (measured at 1024^3 .. 8192^3 for every format). With K in whole 128-byte slices and
+  // 16-byte aligned rows the pipelined direct-to-LDS loops serve everything but the skinny products:
+  //   M <= 128: the skinny kernel (B streamed once, every CU busy);
+  //   at least 128 tiles of 256 x 256 (ragged edges included): 256 x 256 tiles; at half the CUs already 20-40 %
+  //   faster than smaller tiles, whose operands are re-read from L2 twice as often;
+  //   up to 256 tiles of 128 x 128: 128 x 128 tiles, four waves;
+  //   between: 128 x 256 tiles, eight waves (fp8: the register-staged 128 x 128 tiles, as fast there).
+  // Otherwise (K ragged, unaligned rows) the register-staged, bounds-checked tiles, 256 x 256 when there are at
+  // least 256 of them. The 256-row (128-row) operand panels must be addressable by 31-bit buffer offsets.
   const bool vec = kbytes % 16 == 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0;
-  const bool large = big >= 256 && vec;
-  // the pipelined 256 x 256 tiles (ragged M and N too): K in whole 128-byte slices, the 256-row operand panels
-  // addressed by 31-bit buffer offsets
-  const bool whole = vec && kbytes % 128 == 0 && kbytes > 0 && large && 256 * lda <= 0x7fffffff;
-  // few rows: stream B once with every CU busy (whole tiles would leave most CUs idle)
-  const bool skinny = vec && m > 0 && m <= 128 && n > 0 && kbytes % 128 == 0 && kbytes > 0;
-  const bool mid = vec && kbytes % 128 == 0 && kbytes > 0 && ((m + 127) / 128) * ((n + 127) / 128) <= 256 &&
-                   128 * lda <= 0x7fffffff;
+  const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256), t128 = ((m + 127) / 128) * ((n + 127) / 128);
+  const bool piped = vec && kbytes % 128 == 0 && kbytes > 0 && m > 0 && n > 0;
+  const bool skinny = piped && m <= 128;
+  const bool whole = piped && t256 >= 128 && 256 * lda <= 0x7fffffff;
+  const bool mid = piped && t128 <= 256 && 128 * lda <= 0x7fffffff;
+  const bool band = piped && fmt != FMT_FP8 && 256 * ldb <= 0x7fffffff;
+  const bool large = t256 >= 256 && vec;
 #define KRN_GEMM(F)                                                                                    \
-  if (whole) return launch_whole<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                  \
   if (skinny) return launch_skinny<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                \
+  if (whole) return launch_whole<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                  \
   if (mid) return launch_mid<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                      \
+  if (band) return launch_band<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                    \
   return large ? launch_gemm<F, 256, 256, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream)      \
                : launch_gemm<F, 128, 128, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream)
   switch (fmt) {

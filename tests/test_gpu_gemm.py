@@ -135,6 +135,28 @@ RAGGED = [(4000, 4100, 256), (4097, 3969, 128), (3841, 4351, 384)]
 
 # Up to 256 tiles of 128 x 128 (and more than 128 rows) take the pipelined loop on 128 x 128 tiles
 MID = [(1000, 1100, 256), (512, 2048, 384), (1500, 2000, 128)]
+# more than 256 tiles of 128 x 128 but fewer than 128 of 256 x 256: 128 x 256 tiles (fp8: the staged tiles); and
+# from 128 tiles of 256 x 256 on, the 256 x 256 loop with ragged edges
+BAND = [(2560, 2600, 256), (2400, 2900, 128), (3000, 3100, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", BAND)
+def test_bf16_band_sizes_agree_with_the_float64_bound(device, m, n, k):
+    rng = np.random.default_rng(13)
+    (aw, a), (bw, b) = bf16_normal(rng, (m, k)), bf16_normal(rng, (n, k))
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_nt[programs.Tiling(bm=64, bn=64, bk=32)](device.to_device(aw, T.bf16), device.to_device(bw, T.bf16), c)
+    assert_agrees(bf16_values(c.to_host()), a, b.T, k, "bf16")
+
+
+@pytest.mark.parametrize("m,n,k", BAND)
+def test_int8_band_sizes_are_bit_exact(device, m, n, k):
+    rng = np.random.default_rng(14)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    c = device.empty(T.i32, m, n)
+    programs.gemm_i8_i32[programs.Tiling(bm=32, bn=32, bk=32)](device.to_device(a), device.to_device(w), c)
+    np.testing.assert_array_equal(c.to_host(), (a.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64))
 
 
 @pytest.mark.parametrize("m,n,k", MID)
