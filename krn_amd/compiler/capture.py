@@ -78,6 +78,7 @@ UNARY_MATH = {
     "erf": Fn.ERF,
 }  # fmt: skip
 BINARY_MATH = {"maximum": Fn.MAXIMUM, "minimum": Fn.MINIMUM}
+NORMALIZING = ("softmax", "log_softmax")  # take `axis` and keep the shape
 BINOPS = {ast.Add: Op.ADD, ast.Sub: Op.SUB, ast.Mult: Op.MUL, ast.Div: Op.DIV, ast.Mod: Op.MOD}
 CMPOPS = {ast.Lt: Op.LT, ast.LtE: Op.LE, ast.Gt: Op.GT, ast.GtE: Op.GE, ast.Eq: Op.EQ, ast.NotEq: Op.NE}
 
@@ -570,6 +571,11 @@ class Capture:
                 if len(node.args) != 2:
                     raise self.error(node, f"`{name}(a, b)` takes two tiles")
                 return self.math(BINARY_MATH[name], [self.expr(a) for a in node.args], node)
+            case "slice":  # `slice(stop)` or `slice(start, stop)` as a value (reference capture.py:2509-2510)
+                if node.keywords or not 1 <= len(node.args) <= 2:
+                    raise self.error(node, "`slice(start, stop)` takes one or two arguments")
+                lower = node.args[0] if len(node.args) == 2 else None
+                return self.make_slice(lower, node.args[-1], node)
         if dtype_name(func) is not None and dtype_name(func) not in ("int", "float", "bool"):
             return self.dtype_call(D.BY_NAME[dtype_name(func)], node)
         raise self.error(node, f"`{name}(...)` is not captured on the tile path")
@@ -670,7 +676,49 @@ class Capture:
             return self.math(UNARY_MATH[name], [base], node)
         if name in ("max", "min", "sum"):
             return self.reduction(Reduction(name), base, node)
+        if name in NORMALIZING or name in ("logsumexp", "norm"):
+            return self.normalizing(name, base, node)
         raise self.error(node, f"`.{name}()` is not captured on the tile path")
+
+    def normalizing(self, name: str, base: Expr, node: ast.Call) -> Expr:
+        """`x.softmax(axis=1)`, `x.log_softmax(axis)`, `x.logsumexp(axis, keepdims)`, `x.norm(axis, keepdims)`:
+        built from max, sum, exp, log and sqrt as the reference builds them (capture.py:2883-2917); softmax and
+        log_softmax keep the shape, the default axis is the last."""
+        names = ("axis",) if name in NORMALIZING else ("axis", "keepdims")
+        args = dict(zip(names, node.args)) | {k.arg: k.value for k in node.keywords}
+        if set(args) - set(names):
+            raise self.error(node, f"`.{name}()` takes {' and '.join(names)}")
+        axis = int(self.constant(args["axis"], "an axis")) if "axis" in args else -1
+        keepdims = bool(self.constant(args["keepdims"], "keepdims")) if "keepdims" in args else False
+        rank = len(base.shape)
+        if not rank:
+            raise self.error(node, f".{name}() reduces a tile, got {base.type}")
+        if not -rank <= axis < rank:
+            raise self.error(node, f"axis {axis} is out of range for a rank-{rank} tile")
+        if not base.dtype.is_float:
+            raise self.error(node, f".{name}() needs a float tile, got {base.type}")
+        axis %= rank
+
+        def reduce(op: Reduction, x: Expr, keep: bool) -> Expr:
+            shape = x.shape[:axis] + ((1,) if keep else ()) + x.shape[axis + 1:]
+            if not shape:
+                raise self.error(node, "reducing a rank-1 tile to a scalar is not supported; pass keepdims=True")
+            return Reduce(TileType(x.dtype, shape), op, x, axis, keep, line=node.lineno)
+
+        def shifted() -> Expr:  # e^(x - max), the stable exponent shared by softmax and logsumexp
+            return self.math(Fn.EXP, [self.binary(Op.SUB, base, reduce(Reduction.MAX, base, True), node)], node)
+
+        if name == "softmax":
+            return self.binary(Op.DIV, shifted(), reduce(Reduction.SUM, shifted(), True), node)
+        if name == "log_softmax":
+            top = reduce(Reduction.MAX, base, True)
+            logsum = self.math(Fn.LOG, [reduce(Reduction.SUM, shifted(), True)], node)
+            return self.binary(Op.SUB, base, self.binary(Op.ADD, logsum, top, node), node)
+        if name == "logsumexp":
+            top = reduce(Reduction.MAX, base, keepdims)
+            return self.binary(Op.ADD, self.math(Fn.LOG, [reduce(Reduction.SUM, shifted(), keepdims)], node), top,
+                               node)
+        return self.math(Fn.SQRT, [reduce(Reduction.SUM, self.binary(Op.MUL, base, base, node), keepdims)], node)
 
     def single(self, node: ast.Call) -> Expr:
         if len(node.args) + len(node.keywords) != 1:

@@ -8,7 +8,7 @@ kernels mirror the operations of reference tests/kernels/tile_ops.py. `matmul_ep
 3.12 syntax, so it is stated here once per dtype it runs with (f16 and f32).
 """
 
-from krn_amd import Const, Matrix, T, Tensor, Vector, arange, block, kernel, pipelined, struct, where, zeros
+from krn_amd import Const, Matrix, T, Tensor, Vector, arange, block, kernel, maximum, pipelined, struct, where, zeros
 
 
 @struct
@@ -280,3 +280,42 @@ def matmul_epilogue_f32(
     if t.silu:
         acc = acc.silu()
     out[rows, cols] = acc.to(out.dtype)
+
+
+# krn's softmax programs (reference examples/02_tiles_and_types/01_softmax_rows.py:27-40 and
+# tests/helpers/example_softmax.py:12-24), unchanged
+
+
+@struct
+class RowTiling:
+    rows: Const[int] = 4
+    cols: Const[int] = 1024
+
+
+@kernel
+def softmax_long_rows(t: RowTiling, x: Matrix[T.f16], y: Matrix[T.f16]) -> None:
+    rows = block.tile(t.rows)
+    m = zeros(T.f32, t.rows, 1).sub(3.0e38)  # a finite stand-in for -inf, which a kernel cannot spell yet
+    s = zeros(T.f32, t.rows, 1)
+    for cs in pipelined(x.shape[1], t.cols):  # column chunks, the last one ragged
+        v = x[rows, cs].to(T.f32)
+        m_new = maximum(m, v.max(keepdims=True))
+        s = s * (m - m_new).exp() + (v - m_new).exp().sum(keepdims=True)
+        m = m_new
+    for cs in pipelined(x.shape[1], t.cols):
+        y[rows, cs] = (x[rows, cs].to(T.f32) - m).exp().div(s).to(T.f16)
+
+
+@kernel
+def softmax(x: Matrix[T.f16], y: Matrix[T.f16], t: RowTiling) -> None:
+    rows, cols = block.tile(t.rows), slice(0, t.cols)
+    y[rows, cols] = x[rows, cols].to(T.f32).softmax(axis=1).to(T.f16)
+
+
+@kernel
+def softmax_steps(x: Matrix[T.f16], y: Matrix[T.f16], t: RowTiling) -> None:
+    """The same function with its arithmetic spelled out: subtract the row maximum, exponentiate, normalize."""
+    rows, cols = block.tile(t.rows), slice(0, t.cols)
+    v = x[rows, cols].to(T.f32)
+    e = (v - v.max(axis=1, keepdims=True)).exp()
+    y[rows, cols] = (e / e.sum(axis=1, keepdims=True)).to(T.f16)

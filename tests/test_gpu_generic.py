@@ -85,3 +85,25 @@ def test_flash_attention_with_a_small_head_dimension_runs_generic_and_matches_th
     want = np.zeros((heads, seq, d), np.float16)
     emulate.run(capture(KERNELS, "flash_attention", consts={"t": consts}), launch, [q, k, v, want, scale])
     np.testing.assert_allclose(o.to_host().astype(np.float32), want.astype(np.float32), atol=1e-3)
+
+
+@pytest.mark.parametrize("name,rows,cols,tile_cols", [("softmax_long_rows", 6, 2500, 1024),
+                                                      ("softmax_long_rows", 37, 5000, 1024), ("softmax", 6, 512, 512),
+                                                      ("softmax_steps", 9, 4096, 4096)])
+def test_softmax_programs_match_the_c_oracle(device, name, rows, cols, tile_cols):
+    """krn's softmax programs (reference examples/02_tiles_and_types/01_softmax_rows.py, the long rows in ragged
+    column chunks; tests/helpers/example_softmax.py) on the generic lowering against the oracle C backend: the same
+    f32 arithmetic, so f16 results within an ulp (exp differs between the GPU and glibc in the last bits)."""
+    rng = np.random.default_rng(rows * cols)
+    x = (rng.standard_normal((rows, cols)) * 4).astype(np.float16)
+    tiling = programs.RowTiling(rows=4, cols=tile_cols)
+    y = device.empty(T.f16, rows, cols)
+    launch = Blocks(-(-rows // 4))
+    if name == "softmax_long_rows":
+        programs.softmax_long_rows(tiling, device.to_device(x), y, launch=launch)
+    else:
+        getattr(programs, name)(device.to_device(x), y, tiling, launch=launch)
+    kernel = capture(KERNELS, name, consts={"t": {"rows": 4, "cols": tile_cols}})
+    want = np.zeros((rows, cols), np.float16)
+    cbackend.run(kernel, launch, [x, want])
+    np.testing.assert_allclose(y.to_host().astype(np.float32), want.astype(np.float32), rtol=2e-3, atol=2e-6)

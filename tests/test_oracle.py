@@ -205,6 +205,27 @@ def test_flash_attention_on_both_oracles_matches_a_float64_softmax(seq, heads, d
         np.testing.assert_allclose(out.astype(np.float64), want, atol=3e-3)
 
 
+def float64_softmax(x: np.ndarray) -> np.ndarray:
+    v = x.astype(np.float64)
+    e = np.exp(v - v.max(axis=1, keepdims=True))
+    return e / e.sum(axis=1, keepdims=True)
+
+
+@pytest.mark.parametrize("name,rows,cols,tile_cols", [("softmax_long_rows", 6, 2500, 1024), ("softmax", 6, 512, 512),
+                                                      ("softmax_steps", 5, 256, 256)])
+def test_softmax_programs_on_both_oracles_match_a_float64_softmax(name, rows, cols, tile_cols):
+    """krn's softmax programs (reference examples/02_tiles_and_types/01_softmax_rows.py:27-40, 44-53: 6 rows of
+    2500 columns, two full chunks and a ragged one, atol 1e-3 against numpy; tests/helpers/example_softmax.py)."""
+    rng = np.random.default_rng(rows + cols)
+    x = (rng.standard_normal((rows, cols)) * 4).astype(np.float16)
+    kernel = capture(KERNELS, name, consts={"t": {"rows": 4, "cols": tile_cols}})
+    want = float64_softmax(x.astype(np.float32))
+    for run in (emulate.run, cbackend.run):
+        y = np.zeros((rows, cols), np.float16)
+        run(kernel, Blocks(-(-rows // 4)), [x, y])
+        np.testing.assert_allclose(y.astype(np.float64), want, atol=1e-3)
+
+
 def test_int8_products_accumulate_exactly_in_int32_on_both_oracles():
     rng = np.random.default_rng(4)
     a = rng.integers(-127, 128, (33, 70), dtype=np.int8)
