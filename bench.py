@@ -94,6 +94,25 @@ def transpose_copy(device, steps, warmup, rng, n=8192):
     return ms, 2 * n * n
 
 
+def softmax_f16(device, steps, warmup, rng, rows=32768, cols=4096):
+    """krn's row softmax (the kernel its softmax tile programs lower to) over rows x cols f16: 256 MiB read and
+    256 MiB written, twice the 256 MiB last-level cache, so every step streams from HBM."""
+    from krn_amd import T
+    from krn_amd.dtypes import F16
+    from krn_amd.runtime import library
+
+    x = device.to_device((rng.standard_normal((rows, cols), dtype=np.float32) * 4).astype(np.float16))
+    y = device.empty(T.f16, rows, cols)
+    stream = device.default_stream
+
+    def run():
+        library.softmax_rows(F16, x.pointer, y.pointer, rows, cols, cols, cols, stream.handle)
+
+    for _ in range(warmup):
+        run()
+    return events_ms(stream, run, steps), 2 * 2 * rows * cols
+
+
 def vendor_gemm_bf16(steps, warmup, n=8192):
     """The same bf16 product through torch.matmul (hipBLASLt): a reference point for the headline, never the
     product (krn_amd itself does not use torch)."""
@@ -194,7 +213,7 @@ def main() -> None:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    parser.add_argument("--only", default="", help="comma list of extra legs to run (fa, fp8, int8, copy, "
+    parser.add_argument("--only", default="", help="comma list of extra legs to run (fa, fp8, int8, softmax, copy, "
                         "blas); copy (the known-size calibration kernel for HBM byte counters) and blas (the same bf16 "
                         "product through torch/hipBLASLt, a vendor reference point) run only when named")
     args = parser.parse_args()
@@ -210,7 +229,7 @@ def main() -> None:
     print("[bench] bf16 gemm 8192^3", file=sys.stderr, flush=True)
     ms, flops, (a, b, c) = gemm_bf16(device, args.steps, args.warmup, rng)
     tflops = flops / ms / 1e9
-    legs = set(filter(None, args.only.split(","))) or {"fa", "fp8", "int8"}
+    legs = set(filter(None, args.only.split(","))) or {"fa", "fp8", "int8", "softmax"}
     extra = {}
     if "fa" in legs:
         print("[bench] causal bf16 flash attention", file=sys.stderr, flush=True)
@@ -234,6 +253,11 @@ def main() -> None:
                 "ms": round(i_ms, 4), "tops": round(i_ops / i_ms / 1e9, 1),
                 "frac_of_int8_peak": round(i_ops / i_ms / 1e9 / PEAK["int8"], 4),
                 "gbps": round(i_bytes / i_ms / 1e6, 1), "frac_of_hbm": round(i_bytes / i_ms / 1e6 / HBM_PEAK, 4)}
+    if "softmax" in legs:
+        print("[bench] f16 row softmax 32768x4096", file=sys.stderr, flush=True)
+        s_ms, s_bytes = softmax_f16(device, args.steps, args.warmup, rng)
+        extra["softmax_rows_f16_32768x4096"] = {"ms": round(s_ms, 4), "gbps": round(s_bytes / s_ms / 1e6, 1),
+                                                "frac_of_hbm": round(s_bytes / s_ms / 1e6 / HBM_PEAK, 4)}
     if "copy" in legs:
         print("[bench] 16-bit transpose 8192^2 (counter calibration)", file=sys.stderr, flush=True)
         c_ms, c_bytes = transpose_copy(device, args.steps, args.warmup, rng)

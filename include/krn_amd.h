@@ -60,6 +60,15 @@ int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void*
 int krn_attention_fwd(int kind, const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t sq,
                       int64_t sk, int64_t d, float scale, int causal, void* stream);
 
+/* Row softmax: y[r, c] = exp(x[r, c] - max) / sum exp(x[r, :] - max) over the first `width` columns of each of
+ * `rows` rows, float32 arithmetic, one rounding to the element kind (KRN_F32, KRN_F16 or KRN_BF16, the same for x
+ * and y). ldx / ldy are the row strides in elements (>= width); columns past width are neither read nor written.
+ * Replaces krn's softmax tile programs: the long-row online form, reference examples/02_tiles_and_types/
+ * 01_softmax_rows.py:27-40 (column chunks with a running maximum and sum), and the one-tile forms of
+ * tests/helpers/example_softmax.py:12-24 (`.softmax(axis=1)`, capture rule src/krn/compiler/capture.py:2883-2917). */
+int krn_softmax_rows(int kind, const void* x, void* y, int64_t rows, int64_t width, int64_t ldx, int64_t ldy,
+                     void* stream);
+
 /* The message of the calling thread's last failed call. */
 const char* krn_amd_last_error(void);
 

@@ -12,6 +12,9 @@ What `lower` returns is a plan the HIP backend launches:
   the program's `bm, bn, bk` change only the grid it asks for, which must cover the output.
 * `AttentionPlan`: krn's flash-attention tile program (reference examples/04_libraries/08_flash_attention.py:35-59)
   with head dimension 64 or 128, f16 or bf16, causal or not -> `krn_attention_fwd`.
+* `SoftmaxPlan`: krn's row-softmax programs, the long-row running form (reference examples/02_tiles_and_types/
+  01_softmax_rows.py:27-40) and the one-tile forms (tests/helpers/example_softmax.py:12-24), f16, bf16 or f32
+  -> `krn_softmax_rows`.
 * `GenericPlan`: any other tile program -> hipgen (HIP C++ compiled by hiprtc).
 
 Replaces the reference's compile-checked HIP renderer (src/krn/compiler/hip.py:20-183), which emitted 16x16x16
@@ -65,6 +68,16 @@ class AttentionPlan:
     d: int
     bq: int
     causal: bool
+
+
+@dataclass(frozen=True)
+class SoftmaxPlan:
+    x: str
+    y: str
+    dtype: Dtype
+    rows: int  # rows per block of the program's grid
+    cols: int  # the one-tile forms' column extent; the long-row form reads every column
+    long_rows: bool
 
 
 @dataclass
@@ -262,7 +275,32 @@ def match_attention(kernel: ir.Kernel) -> AttentionPlan | None:
                          int(values["bq"]), bool(values["causal"]))
 
 
-def lower(kernel: ir.Kernel) -> GemmPlan | AttentionPlan | GenericPlan:
-    """The plan for `kernel` on gfx950: a hand-written MFMA kernel when the program is one they serve, otherwise
-    the generic HIP lowering."""
-    return match_gemm(kernel) or match_attention(kernel) or GenericPlan(kernel)
+def match_softmax(kernel: ir.Kernel) -> SoftmaxPlan | None:
+    """One of krn's row-softmax programs, recognised like the attention program: the IR compared with the canonical
+    program's IR for the same tiling and element type, after positional renaming."""
+    from krn_amd.compiler import programs
+
+    tensors = [(n, t) for n, t in kernel.params if isinstance(t, ir.TensorType)]
+    if len(tensors) != 2 or len(kernel.params) != 2 or any(t.rank != 2 for _, t in tensors):
+        return None
+    dtype = tensors[0][1].dtype
+    if dtype not in (F16, BF16, F32) or tensors[1][1].dtype != dtype:
+        return None
+    consts = dict(kernel.consts)
+    if len(consts) != 1:
+        return None
+    values = dict(next(iter(consts.values())))
+    if set(values) != {"rows", "cols"} or not all(isinstance(v, int) and v > 0 for v in values.values()):
+        return None
+    form = programs.canonical_form(kernel)
+    for name in programs.SOFTMAX_PROGRAMS:
+        if form == programs.canonical_form(programs.softmax(name, values, dtype)):
+            return SoftmaxPlan(tensors[0][0], tensors[1][0], dtype, int(values["rows"]), int(values["cols"]),
+                               name == "softmax_long_rows")
+    return None
+
+
+def lower(kernel: ir.Kernel) -> GemmPlan | AttentionPlan | SoftmaxPlan | GenericPlan:
+    """The plan for `kernel` on gfx950: a hand-written kernel when the program is one they serve, otherwise the
+    generic HIP lowering."""
+    return match_gemm(kernel) or match_attention(kernel) or match_softmax(kernel) or GenericPlan(kernel)

@@ -8,6 +8,8 @@ from krn_amd.compiler import ir
 from krn_amd.dtypes import F16, Dtype
 
 ATTENTION = Path(__file__).with_name("attention_program.py")
+SOFTMAX = Path(__file__).with_name("softmax_program.py")
+SOFTMAX_PROGRAMS = ("softmax_long_rows", "softmax", "softmax_steps")
 
 
 @cache
@@ -24,6 +26,34 @@ def attention(values: dict, dtype: Dtype) -> ir.Kernel:
     if dtype == F16:
         return kernel
     return _retype(kernel, F16, dtype)
+
+
+@cache
+def _softmax(name: str, items: tuple) -> ir.Kernel:  # captured in f16, as written
+    from krn_amd.compiler.capture import capture
+
+    return capture(SOFTMAX, name, consts={"t": dict(items)})
+
+
+def softmax(name: str, values: dict, dtype: Dtype) -> ir.Kernel:
+    """The canonical row-softmax program `name` for one tiling, with `dtype` tensors (f16 in the source; the
+    `.to(T.f16)` casts follow the tensors)."""
+    kernel = _softmax(name, tuple(sorted(values.items())))
+    if dtype == F16:
+        return kernel
+    return _drop_same_casts(_retype(kernel, F16, dtype))
+
+
+def _drop_same_casts(node):
+    """`node` without casts to the type their operand already has (capture emits none of those)."""
+    if isinstance(node, tuple):
+        return tuple(_drop_same_casts(x) for x in node)
+    if isinstance(node, ir.Cast) and node.operand.dtype == node.dtype:
+        return _drop_same_casts(node.operand)
+    if dataclasses.is_dataclass(node) and not isinstance(node, type):
+        changes = {f.name: _drop_same_casts(getattr(node, f.name)) for f in dataclasses.fields(node)}
+        return dataclasses.replace(node, **changes)
+    return node
 
 
 def _retype(node, old: Dtype, new: Dtype):

@@ -174,6 +174,7 @@ class Kernel:
         self.fn = fn
         self.name = getattr(fn, "__name__", type(fn).__name__)
         self._config: type | None | bool = False
+        self.arity = len(inspect.signature(fn).parameters)
 
     def configuration(self) -> type | None:
         """The `@struct` class of the first parameter, if the kernel is configured."""
@@ -188,8 +189,7 @@ class Kernel:
 
         launcher = Device.current().launcher(self, launch.blocks if isinstance(launch, Tiles) else launch)
         config = self.configuration()
-        arity = len(inspect.signature(self.fn).parameters)
-        if config is not None and len(args) + len(kwargs) == arity - 1:
+        if config is not None and len(args) + len(kwargs) == self.arity - 1:
             launcher = Configured(launcher, config())
         return launcher(*args, **kwargs)
 

@@ -227,6 +227,8 @@ class Launch:
             return
         if isinstance(plan, cdna4.AttentionPlan) and self._attention(plan, params, grid, stream):
             return
+        if isinstance(plan, cdna4.SoftmaxPlan) and self._softmax(plan, params, grid, stream):
+            return
         self._generic(values, grid, stream)
 
     def _gemm(self, plan: cdna4.GemmPlan, params: dict, grid: Blocks, stream: HIPStream) -> bool:
@@ -278,6 +280,15 @@ class Launch:
                               float(np.float32(params[plan.scale])), plan.causal, stream.handle)
         return True
 
+    def _softmax(self, plan: cdna4.SoftmaxPlan, params: dict, grid: Blocks, stream: HIPStream) -> bool:
+        x, y = params[plan.x], params[plan.y]
+        if x.shape != y.shape or (grid.x, grid.y, grid.z) != (-(-x.shape[0] // plan.rows), 1, 1):
+            return False  # not one block per row group over the whole tensor: the generic lowering keeps its meaning
+        rows, cols = x.shape
+        width = cols if plan.long_rows else min(cols, plan.cols)
+        library.softmax_rows(plan.dtype, x.pointer, y.pointer, rows, width, cols, cols, stream.handle)
+        return True
+
     def _generic(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
         program = generic_program(self.kernel)
         params: list = []
@@ -322,14 +333,16 @@ def _scalar_value(e: ir.Expr, params: dict) -> np.float32:
     raise ValueError(f"{type(e).__name__} is not a scalar epilogue operand")
 
 
+_plans: dict[tuple, Launch] = {}  # (kernel, argument kinds) -> its captured IR and plan
+_plans_lock = threading.Lock()
+
+
 class HIPLauncher(Launcher):
     """A kernel with an optional explicit geometry. The first call of a signature captures and plans it."""
 
     def __init__(self, device: "HIPDevice", kernel: Kernel, launch: Blocks | None) -> None:
         self.device, self.kernel, self.launch = device, kernel, launch
         self.parameters = tuple(inspect.signature(kernel.fn).parameters)
-        self._plans: dict[tuple, Launch] = {}
-        self._lock = threading.Lock()
 
     def ordered(self, args: tuple, kwargs: dict) -> tuple:
         if not kwargs and len(args) == len(self.parameters):
@@ -343,20 +356,21 @@ class HIPLauncher(Launcher):
         return ordered
 
     def plan(self, args: Sequence[object]) -> Launch:
-        signature = tuple(map(_kind, args))
+        # launchers are made per call (`k(..., launch=...)`, `k[config]`): the plans live with the process
+        signature = (self.kernel, *map(_kind, args))
         try:
-            return self._plans[signature]
+            return _plans[signature]
         except KeyError:
             pass
-        with self._lock:
-            if signature not in self._plans:
+        with _plans_lock:
+            if signature not in _plans:
                 consts = {n: const_fields(a) for n, a in zip(self.parameters, args)
                           if is_dataclass(a) and not isinstance(a, type)}
                 dtypes = {n: a.dtype for n, a in zip(self.parameters, args) if isinstance(a, HIPTensor)}
                 path = Path(inspect.getsourcefile(self.kernel.fn))
                 kernel = capture(path, self.kernel.name, consts=consts, dtypes=dtypes)
-                self._plans[signature] = Launch(kernel, cdna4.lower(kernel))
-            return self._plans[signature]
+                _plans[signature] = Launch(kernel, cdna4.lower(kernel))
+            return _plans[signature]
 
     def encode(self, args: tuple) -> Callable[[HIPStream], None]:
         launch = self.plan(args)

@@ -41,6 +41,8 @@ def lib() -> ctypes.CDLL:
     ]  # fmt: skip
     handle.krn_transpose16.restype = c_int
     handle.krn_transpose16.argtypes = [c_void_p, c_void_p, c_int64, c_int64, c_void_p]
+    handle.krn_softmax_rows.restype = c_int
+    handle.krn_softmax_rows.argtypes = [c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]
     return handle
 
 
@@ -76,3 +78,8 @@ def attention_fwd(dtype: Dtype, q: int, k: int, v: int, o: int, bh: int, sq: int
 def transpose16(src: int, dst: int, rows: int, cols: int, stream: int) -> None:
     """dst (cols x rows) = src (rows x cols) transposed, 16-bit elements."""
     check(lib().krn_transpose16(src, dst, rows, cols, stream), "krn_transpose16")
+
+
+def softmax_rows(dtype: Dtype, x: int, y: int, rows: int, width: int, ldx: int, ldy: int, stream: int) -> None:
+    """y = softmax over the first `width` columns of each row of x (row strides ldx, ldy in elements)."""
+    check(lib().krn_softmax_rows(kind(dtype), x, y, rows, width, ldx, ldy, stream), "krn_softmax_rows")

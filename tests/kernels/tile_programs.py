@@ -319,3 +319,32 @@ def softmax_steps(x: Matrix[T.f16], y: Matrix[T.f16], t: RowTiling) -> None:
     v = x[rows, cols].to(T.f32)
     e = (v - v.max(axis=1, keepdims=True)).exp()
     y[rows, cols] = (e / e.sum(axis=1, keepdims=True)).to(T.f16)
+
+
+# the same programs written for bf16 and f32 tensors
+
+
+@kernel
+def softmax_long_rows_bf16(t: RowTiling, x: Matrix[T.bf16], y: Matrix[T.bf16]) -> None:
+    rows = block.tile(t.rows)
+    m = zeros(T.f32, t.rows, 1).sub(3.0e38)
+    s = zeros(T.f32, t.rows, 1)
+    for cs in pipelined(x.shape[1], t.cols):
+        v = x[rows, cs].to(T.f32)
+        m_new = maximum(m, v.max(keepdims=True))
+        s = s * (m - m_new).exp() + (v - m_new).exp().sum(keepdims=True)
+        m = m_new
+    for cs in pipelined(x.shape[1], t.cols):
+        y[rows, cs] = (x[rows, cs].to(T.f32) - m).exp().div(s).to(T.bf16)
+
+
+@kernel
+def softmax_bf16(x: Matrix[T.bf16], y: Matrix[T.bf16], t: RowTiling) -> None:
+    rows, cols = block.tile(t.rows), slice(0, t.cols)
+    y[rows, cols] = x[rows, cols].to(T.f32).softmax(axis=1).to(T.bf16)
+
+
+@kernel
+def softmax_f32(x: Matrix[T.f32], y: Matrix[T.f32], t: RowTiling) -> None:
+    rows, cols = block.tile(t.rows), slice(0, t.cols)
+    y[rows, cols] = x[rows, cols].to(T.f32).softmax(axis=1).to(T.f32)

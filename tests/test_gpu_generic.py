@@ -87,18 +87,21 @@ def test_flash_attention_with_a_small_head_dimension_runs_generic_and_matches_th
     np.testing.assert_allclose(o.to_host().astype(np.float32), want.astype(np.float32), atol=1e-3)
 
 
+@pytest.mark.parametrize("path", ["kernel", "generic"])
 @pytest.mark.parametrize("name,rows,cols,tile_cols", [("softmax_long_rows", 6, 2500, 1024),
                                                       ("softmax_long_rows", 37, 5000, 1024), ("softmax", 6, 512, 512),
-                                                      ("softmax_steps", 9, 4096, 4096)])
-def test_softmax_programs_match_the_c_oracle(device, name, rows, cols, tile_cols):
+                                                      ("softmax_steps", 9, 4096, 4096), ("softmax", 10, 700, 512)])
+def test_softmax_programs_match_the_c_oracle(device, name, rows, cols, tile_cols, path):
     """krn's softmax programs (reference examples/02_tiles_and_types/01_softmax_rows.py, the long rows in ragged
-    column chunks; tests/helpers/example_softmax.py) on the generic lowering against the oracle C backend: the same
-    f32 arithmetic, so f16 results within an ulp (exp differs between the GPU and glibc in the last bits)."""
+    column chunks; tests/helpers/example_softmax.py) against the oracle C backend: the same f32 arithmetic, so f16
+    results within an ulp (exp differs between the GPU and glibc in the last bits). One block per 4 rows takes the
+    row-softmax kernel; one block more keeps the program's own meaning on the generic lowering."""
     rng = np.random.default_rng(rows * cols)
     x = (rng.standard_normal((rows, cols)) * 4).astype(np.float16)
     tiling = programs.RowTiling(rows=4, cols=tile_cols)
     y = device.empty(T.f16, rows, cols)
-    launch = Blocks(-(-rows // 4))
+    y.copy_from(np.zeros((rows, cols), np.float16))
+    launch = Blocks(-(-rows // 4) + (path == "generic"))
     if name == "softmax_long_rows":
         programs.softmax_long_rows(tiling, device.to_device(x), y, launch=launch)
     else:

@@ -45,3 +45,23 @@ def test_attention_program_lowers_to_the_attention_kernel():
     consts = {"t": {"bq": 64, "bk": 64, "d": 128, "causal": True}}
     plan = cdna4.lower(capture(KERNELS, "flash_attention_bf16", consts=consts))
     assert isinstance(plan, cdna4.AttentionPlan) and plan.d == 128 and plan.causal
+
+
+
+@pytest.mark.parametrize("name, long_rows, dtype", [
+    ("softmax_long_rows", True, "f16"), ("softmax", False, "f16"), ("softmax_steps", False, "f16"),
+    ("softmax_long_rows_bf16", True, "bf16"), ("softmax_bf16", False, "bf16"), ("softmax_f32", False, "f32"),
+])  # fmt: skip
+def test_softmax_programs_lower_to_the_row_softmax_kernel(name, long_rows, dtype):
+    from krn_amd.dtypes import BF16, F16, F32
+
+    dt = {"f16": F16, "bf16": BF16, "f32": F32}[dtype]
+    plan = cdna4.lower(capture(KERNELS, name, consts={"t": {"rows": 4, "cols": 512}}))
+    assert isinstance(plan, cdna4.SoftmaxPlan)
+    assert (plan.x, plan.y, plan.dtype, plan.rows, plan.cols, plan.long_rows) == ("x", "y", dt, 4, 512, long_rows)
+
+
+def test_a_softmax_over_fixed_rows_lowers_generically():
+    """`row_softmax` reads rows 0..rows-1 in every block, not the block's own rows: not the kernel's function."""
+    plan = cdna4.lower(capture(KERNELS, "row_softmax", consts={"t": {"rows": 4, "cols": 512}}))
+    assert isinstance(plan, cdna4.GenericPlan)
