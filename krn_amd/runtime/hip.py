@@ -28,7 +28,7 @@ from krn_amd.compiler import ir
 from krn_amd.compiler.capture import TargetError, capture
 from krn_amd.dtypes import BF16, F32, Dtype
 from krn_amd.frontend import Blocks, Kernel, Tensor, const_fields
-from krn_amd.runtime import api, hipapi, library
+from krn_amd.runtime import api, hipapi, library, roctx
 from krn_amd.runtime.api import Backend, Bound, Device, Event, Graph, Launcher, Stream, current_stream
 
 TARGET = "gfx950"
@@ -221,6 +221,13 @@ class Launch:
         self.kernel, self.plan = kernel, plan
 
     def run(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
+        if not roctx.launch_ranges():
+            self._run(values, grid, stream)
+            return
+        with roctx.span(f"krn:{self.kernel.name} {type(self.plan).__name__}"):
+            self._run(values, grid, stream)
+
+    def _run(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
         params = dict(zip((name for name, _ in self.kernel.params), values))
         plan = self.plan
         if isinstance(plan, cdna4.GemmPlan) and self._gemm(plan, params, grid, stream):
