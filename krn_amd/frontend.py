@@ -174,7 +174,8 @@ class Kernel:
         self.fn = fn
         self.name = getattr(fn, "__name__", type(fn).__name__)
         self._config: type | None | bool = False
-        self.arity = len(inspect.signature(fn).parameters)
+        self.parameters = tuple(inspect.signature(fn).parameters)
+        self.arity = len(self.parameters)
 
     def configuration(self) -> type | None:
         """The `@struct` class of the first parameter, if the kernel is configured."""

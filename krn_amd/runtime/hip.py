@@ -349,7 +349,7 @@ class HIPLauncher(Launcher):
 
     def __init__(self, device: "HIPDevice", kernel: Kernel, launch: Blocks | None) -> None:
         self.device, self.kernel, self.launch = device, kernel, launch
-        self.parameters = tuple(inspect.signature(kernel.fn).parameters)
+        self.parameters = kernel.parameters
 
     def ordered(self, args: tuple, kwargs: dict) -> tuple:
         if not kwargs and len(args) == len(self.parameters):
