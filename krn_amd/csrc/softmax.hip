@@ -57,6 +57,10 @@ __device__ __forceinline__ void load8(const void* X, int64_t row, int64_t ld, in
   }
 }
 
+// Whole 16-bit chunks (one 16-byte store per lane, lanes contiguous) are stored non-temporally: the output is not read
+// again by this kernel, and keeping it out of the caches' way lifts f16 32768 x 4096 from 5.0 to 6.5 TB/s. float32
+// chunks are two 16-byte stores 32 bytes apart per lane, half lines per instruction, which are slower non-temporal
+// (8192 x 4096: 0.047 -> 0.067 ms), so they keep ordinary stores.
 template <int KIND>
 __device__ __forceinline__ void store8(void* Y, int64_t row, int64_t ld, int64_t c, int64_t width, bool vec,
                                        const float* v) {
@@ -74,7 +78,8 @@ __device__ __forceinline__ void store8(void* Y, int64_t row, int64_t ld, int64_t
         const uint32_t hi = KIND == F16 ? f2h(v[2 * q + 1]) : f2bf(v[2 * q + 1]);
         w[q] = lo | (hi << 16);
       }
-      *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(Y) + row * ld + col) = u32x4{w[0], w[1], w[2], w[3]};
+      __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]},
+                                  reinterpret_cast<u32x4*>(static_cast<uint16_t*>(Y) + row * ld + col));
     }
     return;
   }
