@@ -9,7 +9,7 @@
 // maximum or the sum.
 //
 // Layout (HBM-bound: one read, one write per element). One wave per row, four rows per workgroup, no LDS and no
-// barriers (or, for fewer than 4096 rows longer than 2048 columns, four waves per row): lane l owns the 8-element
+// barriers (or, for at most 4096 rows longer than 2048 columns, four waves per row): lane l owns the 8-element
 // chunks l, l + 64, ...; it keeps a running maximum m and sum s of its chunks (s rescaled by exp(m_old - m_new)
 // when m grows), the wave combines the 64 pairs by shuffles, and a second pass writes exp(x - m) * (1 / s). Up to
 // CACHE chunks per lane stay in registers between the passes, so those rows are read from HBM once; longer rows
@@ -186,7 +186,7 @@ template <int KIND>
 static int launch_softmax(const void* x, void* y, int64_t rows, int64_t width, int64_t ldx, int64_t ldy,
                           hipStream_t stream) {
   const dim3 block(256);
-  if (rows < 4096 && width > 2048) {
+  if (rows <= 4096 && width > 2048) {
     // few long rows: a workgroup per row; up to 16384 columns stay in registers between the passes
     hipLaunchKernelGGL((softmax_rows<KIND, 8, 4>), dim3((unsigned)rows), block, 0, stream, x, y, rows, width, ldx,
                        ldy);
