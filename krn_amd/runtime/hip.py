@@ -220,25 +220,37 @@ class Launch:
     def __init__(self, kernel: ir.Kernel, plan) -> None:
         self.kernel, self.plan = kernel, plan
 
-    def run(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
-        if not roctx.launch_ranges():
-            self._run(values, grid, stream)
-            return
-        with roctx.span(f"krn:{self.kernel.name} {type(self.plan).__name__}"):
-            self._run(values, grid, stream)
-
-    def _run(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
+    def prepare(self, values: list[object], grid: Blocks) -> Callable[[HIPStream], None]:
+        """The launch of these argument values on this grid as one call per stream: the plan's checks and argument
+        marshalling run here, once, so a `Bound` replays only the library call."""
         params = dict(zip((name for name, _ in self.kernel.params), values))
         plan = self.plan
-        if isinstance(plan, cdna4.GemmPlan) and self._gemm(plan, params, grid, stream):
-            return
-        if isinstance(plan, cdna4.AttentionPlan) and self._attention(plan, params, grid, stream):
-            return
-        if isinstance(plan, cdna4.SoftmaxPlan) and self._softmax(plan, params, grid, stream):
-            return
-        self._generic(values, grid, stream)
+        call = None
+        if isinstance(plan, cdna4.GemmPlan):
+            call = self._gemm(plan, params, grid)
+        elif isinstance(plan, cdna4.AttentionPlan):
+            call = self._attention(plan, params, grid)
+        elif isinstance(plan, cdna4.SoftmaxPlan):
+            call = self._softmax(plan, params, grid)
+        if call is None:
+            def call(stream: HIPStream) -> None:
+                self._generic(values, grid, stream)
 
-    def _gemm(self, plan: cdna4.GemmPlan, params: dict, grid: Blocks, stream: HIPStream) -> bool:
+        name = f"krn:{self.kernel.name} {type(plan).__name__}"
+
+        def run(stream: HIPStream) -> None:
+            if not roctx.launch_ranges():
+                call(stream)
+                return
+            with roctx.span(name):
+                call(stream)
+
+        return run
+
+    def run(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
+        self.prepare(values, grid)(stream)
+
+    def _gemm(self, plan: cdna4.GemmPlan, params: dict, grid: Blocks):
         a, b, c = params[plan.a], params[plan.b], params[plan.c]
         m, k = a.shape
         n = b.shape[0] if plan.layout == "nt" else b.shape[1]
@@ -246,7 +258,7 @@ class Launch:
         extent = space.extent(plan.loop_extent, params) if isinstance(plan.loop_extent, ir.Dim) else None
         if extent != k or kb != k or c.shape != (m, n) or (grid.x, grid.y, grid.z) != (
                 -(-n // plan.bn), -(-m // plan.bm), 1):
-            return False  # not the whole product: the generic lowering keeps the program's exact meaning
+            return None  # not the whole product: the generic lowering keeps the program's exact meaning
         ops = []
         for op in plan.ops:
             if op.op in library.ACTIVATIONS:
@@ -259,42 +271,44 @@ class Launch:
                 vector = params[op.tensor]
                 wants = [(m, 1)] if op.axis == "row" else [(1, n), (n,)]
                 if vector.shape not in wants or vector.dtype not in library.VECTOR_KINDS:
-                    return False
+                    return None
                 code = base + (1 if op.axis == "row" else 2) + library.VECTOR_KINDS[vector.dtype]
                 ops.append((code, 0.0, vector.pointer))
         if plan.layout == "nn":
-            scratch = self.device_scratch(stream, n * k * 2)
-            library.transpose16(b.pointer, scratch.pointer, k, n, stream.handle)
-            library.gemm_nt(plan.operand, a.pointer, scratch.pointer, c.pointer, plan.output, m, n, k, ops,
-                            stream.handle)
-            stream.note(self.kernel.name, (scratch,))
-        else:
-            library.gemm_nt(plan.operand, a.pointer, b.pointer, c.pointer, plan.output, m, n, k, ops, stream.handle)
-        return True
+            def nn(stream: HIPStream) -> None:
+                scratch = self.device_scratch(stream, n * k * 2)
+                library.transpose16(b.pointer, scratch.pointer, k, n, stream.handle)
+                library.gemm_nt(plan.operand, a.pointer, scratch.pointer, c.pointer, plan.output, m, n, k, ops,
+                                stream.handle)
+                stream.note(self.kernel.name, (scratch,))
+
+            return nn
+        product = library.gemm_nt_call(plan.operand, a.pointer, b.pointer, c.pointer, plan.output, m, n, k, ops)
+        return lambda stream: product(stream.handle)
 
     def device_scratch(self, stream: HIPStream, nbytes: int) -> HIPTensor:
         return stream.device.empty(D.U8, max(nbytes, 1))
 
-    def _attention(self, plan: cdna4.AttentionPlan, params: dict, grid: Blocks, stream: HIPStream) -> bool:
+    def _attention(self, plan: cdna4.AttentionPlan, params: dict, grid: Blocks):
         q, k, v, o = (params[n] for n in (plan.q, plan.k, plan.v, plan.o))
         bh, sq, d = q.shape
         sk = k.shape[1]
         if d != plan.d or k.shape != (bh, sk, d) or v.shape != (bh, sk, d) or o.shape != (bh, sq, d):
-            return False
+            return None
         if (grid.x, grid.y, grid.z) != (-(-sq // plan.bq), bh, 1) or sk == 0:
-            return False
-        library.attention_fwd(plan.dtype, q.pointer, k.pointer, v.pointer, o.pointer, bh, sq, sk, d,
-                              float(np.float32(params[plan.scale])), plan.causal, stream.handle)
-        return True
+            return None
+        scale = float(np.float32(params[plan.scale]))
+        return lambda stream: library.attention_fwd(plan.dtype, q.pointer, k.pointer, v.pointer, o.pointer, bh, sq,
+                                                    sk, d, scale, plan.causal, stream.handle)
 
-    def _softmax(self, plan: cdna4.SoftmaxPlan, params: dict, grid: Blocks, stream: HIPStream) -> bool:
+    def _softmax(self, plan: cdna4.SoftmaxPlan, params: dict, grid: Blocks):
         x, y = params[plan.x], params[plan.y]
         if x.shape != y.shape or (grid.x, grid.y, grid.z) != (-(-x.shape[0] // plan.rows), 1, 1):
-            return False  # not one block per row group over the whole tensor: the generic lowering keeps its meaning
+            return None  # not one block per row group over the whole tensor: the generic lowering keeps its meaning
         rows, cols = x.shape
         width = cols if plan.long_rows else min(cols, plan.cols)
-        library.softmax_rows(plan.dtype, x.pointer, y.pointer, rows, width, cols, cols, stream.handle)
-        return True
+        return lambda stream: library.softmax_rows(plan.dtype, x.pointer, y.pointer, rows, width, cols, cols,
+                                                   stream.handle)
 
     def _generic(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
         program = generic_program(self.kernel)
@@ -384,9 +398,12 @@ class HIPLauncher(Launcher):
         values = space.runtime_args(launch.kernel, args)
         grid = self.launch if self.launch is not None else space.geometry(launch.kernel, values)
 
+        call = launch.prepare(values, grid)
+        keep = tuple(values)
+
         def run(stream: HIPStream) -> None:
-            launch.run(values, grid, stream)
-            stream.note(self.kernel.name, tuple(values))
+            call(stream)
+            stream.note(self.kernel.name, keep)
 
         return run
 

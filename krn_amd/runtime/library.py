@@ -58,15 +58,26 @@ def kind(dtype: Dtype) -> int:
         raise KernelError(f"{dtype} has no kind in the kernel library's C ABI") from None
 
 
-def gemm_nt(in_dtype: Dtype, a: int, b: int, c: int, out_dtype: Dtype, m: int, n: int, k: int,
-            ops: list[tuple[int, float, int]], stream: int) -> None:
-    """C[m, n] = epilogue(sum_k A[m, k] B[n, k]); `ops` are (operation, scalar, vector pointer)."""
+def gemm_nt_call(in_dtype: Dtype, a: int, b: int, c: int, out_dtype: Dtype, m: int, n: int, k: int,
+                 ops: list[tuple[int, float, int]]):
+    """`gemm_nt` of these arguments as a function of the stream, with the arguments marshalled once."""
     count = len(ops)
     codes = (c_int * max(count, 1))(*(op for op, _, _ in ops))
     scalars = (c_float * max(count, 1))(*(s for _, s, _ in ops))
     vectors = (c_void_p * max(count, 1))(*(v for _, _, v in ops))
-    check(lib().krn_gemm_nt(kind(in_dtype), a, b, c, kind(out_dtype), m, n, k, count, codes, scalars, vectors,
-                            stream), "krn_gemm_nt")
+    entry = lib().krn_gemm_nt
+    head = (kind(in_dtype), a, b, c, kind(out_dtype), m, n, k, count, codes, scalars, vectors)
+
+    def call(stream: int) -> None:
+        check(entry(*head, stream), "krn_gemm_nt")
+
+    return call
+
+
+def gemm_nt(in_dtype: Dtype, a: int, b: int, c: int, out_dtype: Dtype, m: int, n: int, k: int,
+            ops: list[tuple[int, float, int]], stream: int) -> None:
+    """C[m, n] = epilogue(sum_k A[m, k] B[n, k]); `ops` are (operation, scalar, vector pointer)."""
+    gemm_nt_call(in_dtype, a, b, c, out_dtype, m, n, k, ops)(stream)
 
 
 def attention_fwd(dtype: Dtype, q: int, k: int, v: int, o: int, bh: int, sq: int, sk: int, d: int, scale: float,
