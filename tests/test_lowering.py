@@ -65,3 +65,30 @@ def test_a_softmax_over_fixed_rows_lowers_generically():
     """`row_softmax` reads rows 0..rows-1 in every block, not the block's own rows: not the kernel's function."""
     plan = cdna4.lower(capture(KERNELS, "row_softmax", consts={"t": {"rows": 4, "cols": 512}}))
     assert isinstance(plan, cdna4.GenericPlan)
+
+
+def test_softmax_launch_passes_the_row_width_and_refuses_other_grids(monkeypatch):
+    """Host side of the row-softmax launch: width min(cols, t.cols) for the one-tile forms and every column for the
+    long-row form, one stride per row; a grid other than one block per t.rows rows, or x and y of different shapes,
+    keeps the generic lowering."""
+    from types import SimpleNamespace
+
+    from krn_amd import Blocks
+    from krn_amd.runtime import hip, library
+
+    calls = []
+    monkeypatch.setattr(library, "softmax_rows", lambda *a: calls.append(a))
+    stream = SimpleNamespace(handle=7)
+    for name, cols, width in [("softmax", 700, 512), ("softmax", 300, 300), ("softmax_long_rows", 3000, 3000)]:
+        kernel = capture(KERNELS, name, consts={"t": {"rows": 4, "cols": 512}})
+        plan = cdna4.lower(kernel)
+        launch = hip.Launch(kernel, plan)
+        x = SimpleNamespace(shape=(10, cols), pointer=100)
+        y = SimpleNamespace(shape=(10, cols), pointer=200)
+        params = {"x": x, "y": y}
+        run = launch._softmax(plan, params, Blocks(3))
+        run(stream)
+        assert calls[-1][1:] == (100, 200, 10, width, cols, cols, 7)
+        assert launch._softmax(plan, params, Blocks(4)) is None
+        assert launch._softmax(plan, {"x": x, "y": SimpleNamespace(shape=(10, cols + 1), pointer=200)},
+                               Blocks(3)) is None
