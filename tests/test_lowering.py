@@ -92,3 +92,39 @@ def test_softmax_launch_passes_the_row_width_and_refuses_other_grids(monkeypatch
         assert launch._softmax(plan, params, Blocks(4)) is None
         assert launch._softmax(plan, {"x": x, "y": SimpleNamespace(shape=(10, cols + 1), pointer=200)},
                                Blocks(3)) is None
+
+
+def test_gemm_launch_marshals_once_and_refuses_partial_grids(monkeypatch):
+    """The W8A8 program's launch: the row and column scale vectors become epilogue operations 1 and 2 (float32),
+    the arguments are marshalled once at preparation, and a grid that does not cover the output keeps the generic
+    lowering."""
+    from types import SimpleNamespace
+
+    from krn_amd import Blocks
+    from krn_amd.dtypes import F32
+    from krn_amd.runtime import hip, library
+
+    made, ran = [], []
+
+    def gemm_nt_call(*args):
+        made.append(args)
+        return lambda stream: ran.append(stream)
+
+    monkeypatch.setattr(library, "gemm_nt_call", gemm_nt_call)
+    kernel = capture(KERNELS, "gemm_w8a8", consts={"t": {"bm": 64, "bn": 64, "bk": 32}})
+    plan = cdna4.lower(kernel)
+    launch = hip.Launch(kernel, plan)
+    m, n, k = 16, 200, 256
+    params = {"a": SimpleNamespace(shape=(m, k), pointer=1), "w": SimpleNamespace(shape=(n, k), pointer=2),
+              "scale_a": SimpleNamespace(shape=(m, 1), pointer=3, dtype=F32),
+              "scale_w": SimpleNamespace(shape=(1, n), pointer=4, dtype=F32),
+              "c": SimpleNamespace(shape=(m, n), pointer=5)}
+    run = launch._gemm(plan, params, Blocks(4, 1))
+    assert len(made) == 1
+    _, a, b, c, _, mm, nn, kk, ops = made[0]
+    assert (a, b, c, mm, nn, kk) == (1, 2, 5, m, n, k)
+    assert ops == [(library.MUL_ROW, 0.0, 3), (library.MUL_COL, 0.0, 4)]
+    for _ in range(3):
+        run(SimpleNamespace(handle=9))
+    assert ran == [9, 9, 9] and len(made) == 1
+    assert launch._gemm(plan, params, Blocks(3, 1)) is None
