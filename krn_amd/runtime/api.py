@@ -11,7 +11,7 @@ import os
 from abc import ABC, abstractmethod
 from collections.abc import Callable
 from contextvars import ContextVar
-from functools import cache, partial
+from functools import partial
 from importlib import import_module
 
 
@@ -209,7 +209,8 @@ class Backend(ABC):
     vendor: str
 
     @abstractmethod
-    def device(self, arch: str) -> Device: ...
+    def device(self, target) -> Device:
+        """The one device of `target`: krn's `Target` (read by `.arch` and `.vendor`) or an arch name."""
 
 
 MODULES = {"amd": "krn_amd.runtime.hip"}
@@ -225,19 +226,43 @@ def target() -> str:
     return os.environ.get("KRN_TARGET", "gfx950")
 
 
+def arch_of(target) -> str:
+    """The arch name of a target: krn's `Target` carries it as `.arch` (reference src/krn/facts/targets.py:99); a
+    plain string is the name itself."""
+    if isinstance(target, str):
+        return target
+    arch = getattr(target, "arch", None)
+    if not isinstance(arch, str):
+        raise TypeError(f"a target is an arch name or an object with an `arch` name, not {type(target).__name__}")
+    return arch
+
+
 def default_device() -> Device:
     return device_of(target())
 
 
-@cache
-def device_of(arch: str) -> Device:
-    """The one device of `arch` for this process; the backend module is imported on first use."""
-    vendor = VENDORS.get(arch)
-    if vendor is None:
+def device_of(target) -> Device:
+    """The one device of `target` (krn's `Target` or its arch name) for this process; the backend module is
+    imported on first use (reference src/krn/runtime/api.py:341-354: the vendor names the module, nothing
+    registers it)."""
+    arch = arch_of(target)
+    vendor = getattr(target, "vendor", None) or VENDORS.get(arch)
+    return _device(arch, vendor, target)
+
+
+_devices: dict[tuple[str, str | None], Device] = {}
+
+
+def _device(arch: str, vendor: str | None, target) -> Device:
+    key = (arch, vendor)
+    if key in _devices:
+        return _devices[key]
+    if vendor not in MODULES:
         raise BackendUnavailable(f"target {arch!r} has no backend in krn_amd; set KRN_TARGET=gfx950")
     try:
         backend: Backend = import_module(MODULES[vendor]).BACKEND
     except (ImportError, AttributeError, OSError) as error:
         raise BackendUnavailable(f"{arch} was selected but its backend {MODULES[vendor]!r} failed to load: {error}") \
             from error
-    return backend.device(arch)
+    _devices[key] = device = backend.device(target)
+    return device

@@ -14,7 +14,9 @@ import hashlib
 import inspect
 import os
 import threading
+import time
 import weakref
+from collections import deque
 from collections.abc import Callable, Sequence
 from ctypes import c_float, c_int, c_int64, c_void_p
 from dataclasses import is_dataclass
@@ -58,6 +60,15 @@ class HIPEvent(Event):
         return self._done
 
     def wait(self, timeout: float | None = None) -> None:
+        """Block until the event completes; with a timeout, poll until the deadline and raise TimeoutError after it
+        (reference runtime/cuda_backend.py:132-142)."""
+        if timeout is not None:
+            deadline = time.monotonic() + timeout
+            while not self.done():
+                if time.monotonic() > deadline:
+                    raise TimeoutError(f"event not completed after {timeout} seconds")
+                time.sleep(1e-4)
+            return
         try:
             hipapi.api().hipEventSynchronize(c_void_p(self.handle))
         except hipapi.HIPError as error:
@@ -98,16 +109,36 @@ class HIPEvent(Event):
             pass
 
 
+KEEP_LIMIT = 256  # launches a stream holds before it records a marker of its own (reference completion.py:19)
+
+
 class HIPStream(Stream):
+    """An in-order queue of device work. A launch's arguments are held until a marker event recorded after it has
+    completed (the `Keeper` of reference runtime/completion.py:99-131): `record()` closes the open launches under its
+    event and releases every older marker that is done, and after KEEP_LIMIT unmarked launches the stream records a
+    marker itself, so a loop that never synchronizes holds a bounded number of them."""
+
     def __init__(self, device: "HIPDevice", handle: int) -> None:
         self.device, self.handle = device, handle
-        self._pending: list[tuple[str, HIPEvent | None]] = []
-        self._keep: list[tuple[object, ...]] = []
+        self._open: list[tuple[str, tuple[object, ...]]] = []
+        self._marks: deque[tuple[HIPEvent, list[tuple[str, tuple[object, ...]]]]] = deque()
+
+    @property
+    def capturing(self) -> bool:
+        return hipapi.capturing(self.handle)
 
     def record(self) -> HIPEvent:
         event = HIPEvent(self.device, hipapi.event_create())
         hipapi.api().hipEventRecord(c_void_p(event.handle), c_void_p(self.handle))
+        if not self.capturing:  # a capture's events cannot be queried; the graph holds what it recorded
+            self._mark(event)
         return event
+
+    def _mark(self, event: HIPEvent) -> None:
+        self._marks.append((event, self._open))
+        self._open = []
+        while self._marks and self._marks[0][0].done():
+            self._marks.popleft()
 
     def wait(self, event: Event) -> None:
         if not isinstance(event, HIPEvent):
@@ -115,27 +146,45 @@ class HIPStream(Stream):
         hipapi.api().hipStreamWaitEvent(c_void_p(self.handle), c_void_p(event.handle), 0)
 
     def pending_launches(self) -> tuple[str, ...]:
-        return tuple(name for name, _ in self._pending)
+        """The launches queued on this stream that have not completed, oldest first: those under markers not yet
+        done, then those not yet under a marker (reference api.py:117-118)."""
+        marked = [name for event, launches in self._marks if not event.done() for name, _ in launches]
+        return (*marked, *(name for name, _ in self._open))
 
     def note(self, name: str, keep: tuple[object, ...]) -> None:
-        """Remember a launch and hold its arguments until the stream is next synchronized."""
-        self._pending.append((name, None))
-        self._keep.append(keep)
+        """Hold a launch's arguments until the work that reads them has completed."""
+        self._open.append((name, keep))
+        if len(self._open) >= KEEP_LIMIT and not self.capturing:
+            self.record()
+
+    def take(self) -> list[tuple[object, ...]]:
+        """Everything held for the launches not yet under a marker, handed over (to a graph that recorded them)."""
+        held = [keep for _, keep in self._open]
+        self._open = []
+        return held
 
     def sync(self) -> None:
         hipapi.api().hipStreamSynchronize(c_void_p(self.handle))
-        self._pending.clear()
-        self._keep.clear()
+        self._open = []
+        self._marks.clear()
 
 
 class HIPTensor(Tensor):
-    """C-contiguous device memory with its element type (bf16 as uint16 words, fp8 as uint8 codes) and shape."""
+    """C-contiguous device memory with its element type (bf16 as uint16 words, fp8 as uint8 codes) and shape.
 
-    def __init__(self, device: "HIPDevice", pointer: int, dtype: Dtype, shape: tuple[int, ...], owner=None) -> None:
+    Memory is stream ordered (reference runtime/cuda_backend.py module doc and 205-248): a tensor is allocated from
+    the device's pool on the stream that was current when it was made, and returned to the pool on that same
+    stream when its last reference goes, so the free waits for the work queued there before it. Work on another
+    stream reaches the tensor after waiting for an event of the allocating stream, and the launches there hold
+    their arguments until they have completed. A tensor made while its stream records a graph is a plain
+    allocation that the graph owns, freed with hipFree."""
+
+    def __init__(self, device: "HIPDevice", pointer: int, dtype: Dtype, shape: tuple[int, ...], owner=None,
+                 stream: "HIPStream | None" = None) -> None:
         self.device, self.pointer, self.dtype, self.shape = device, pointer, dtype, tuple(int(s) for s in shape)
         self.numpy = D.NUMPY[dtype]
         self._owner = owner  # a view keeps the owner alive; an owner frees its memory
-
+        self._stream = stream  # the allocating stream (stream-ordered memory), or None for a plain allocation
     @property
     def nbytes(self) -> int:
         return self.numpy.itemsize * int(np.prod(self.shape))
@@ -166,7 +215,10 @@ class HIPTensor(Tensor):
     def __del__(self) -> None:
         if self._owner is None and self.pointer:
             try:
-                hipapi.free(self.pointer)
+                if self._stream is not None:
+                    hipapi.free_async(self.pointer, self._stream.handle)
+                else:
+                    hipapi.free(self.pointer)
             except Exception:
                 pass
             self.pointer = 0
@@ -194,10 +246,17 @@ class Program:
         hipapi.api().hipModuleGetFunction(ctypes.byref(function), module, entry.encode())
         self.module, self.function, self._buffer = module, function, buffer
 
-    def launch(self, grid: tuple[int, int, int], threads: int, params: list, stream: int) -> None:
-        pointers = (c_void_p * max(len(params), 1))(*(ctypes.cast(ctypes.byref(p), c_void_p) for p in params))
+    @staticmethod
+    def table(params: list) -> ctypes.Array:
+        """The kernelParams table of `params`: the address of each. The table holds the parameter objects too, so
+        the addresses stay valid for as long as the table does."""
+        table = (c_void_p * max(len(params), 1))(*(ctypes.addressof(p) for p in params))
+        table.params = list(params)
+        return table
+
+    def launch(self, grid: tuple[int, int, int], threads: int, table: ctypes.Array, stream: int) -> None:
         hipapi.api().hipModuleLaunchKernel(self.function, grid[0], grid[1], grid[2], threads, 1, 1, 0,
-                                           c_void_p(stream), pointers, None)
+                                           c_void_p(stream), table, None)
 
 
 _programs: dict[str, Program] = {}
@@ -233,8 +292,7 @@ class Launch:
         elif isinstance(plan, cdna4.SoftmaxPlan):
             call = self._softmax(plan, params, grid)
         if call is None:
-            def call(stream: HIPStream) -> None:
-                self._generic(values, grid, stream)
+            call = self._generic(values, grid)
 
         name = f"krn:{self.kernel.name} {type(plan).__name__}"
 
@@ -259,6 +317,8 @@ class Launch:
         if extent != k or kb != k or c.shape != (m, n) or (grid.x, grid.y, grid.z) != (
                 -(-n // plan.bn), -(-m // plan.bm), 1):
             return None  # not the whole product: the generic lowering keeps the program's exact meaning
+        if len(plan.ops) > library.MAX_OPS:
+            return None  # longer epilogue chains than the library's: the generic lowering runs them
         ops = []
         for op in plan.ops:
             if op.op in library.ACTIVATIONS:
@@ -275,19 +335,23 @@ class Launch:
                 code = base + (1 if op.axis == "row" else 2) + library.VECTOR_KINDS[vector.dtype]
                 ops.append((code, 0.0, vector.pointer))
         if plan.layout == "nn":
+            scratch = StreamScratch(n * k * 2)
+
+            products: dict[int, Callable[[int], None]] = {}  # scratch pointer -> the product marshalled for it
+
             def nn(stream: HIPStream) -> None:
-                scratch = self.device_scratch(stream, n * k * 2)
-                library.transpose16(b.pointer, scratch.pointer, k, n, stream.handle)
-                library.gemm_nt(plan.operand, a.pointer, scratch.pointer, c.pointer, plan.output, m, n, k, ops,
-                                stream.handle)
-                stream.note(self.kernel.name, (scratch,))
+                bt = scratch.on(stream)
+                product = products.get(bt.pointer)
+                if product is None:
+                    product = products[bt.pointer] = library.gemm_nt_call(plan.operand, a.pointer, bt.pointer,
+                                                                          c.pointer, plan.output, m, n, k, ops)
+                library.transpose16(b.pointer, bt.pointer, k, n, stream.handle)
+                product(stream.handle)
+                stream.note(self.kernel.name, (bt,))
 
             return nn
         product = library.gemm_nt_call(plan.operand, a.pointer, b.pointer, c.pointer, plan.output, m, n, k, ops)
         return lambda stream: product(stream.handle)
-
-    def device_scratch(self, stream: HIPStream, nbytes: int) -> HIPTensor:
-        return stream.device.empty(D.U8, max(nbytes, 1))
 
     def _attention(self, plan: cdna4.AttentionPlan, params: dict, grid: Blocks):
         q, k, v, o = (params[n] for n in (plan.q, plan.k, plan.v, plan.o))
@@ -310,7 +374,8 @@ class Launch:
         return lambda stream: library.softmax_rows(plan.dtype, x.pointer, y.pointer, rows, width, cols, cols,
                                                    stream.handle)
 
-    def _generic(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
+    def _generic(self, values: list[object], grid: Blocks) -> Callable[[HIPStream], None]:
+        """The hiprtc program of this kernel, compiled (or found) once, with its kernelParams table built once."""
         program = generic_program(self.kernel)
         params: list = []
         for (name, kind), value in zip(self.kernel.params, values):
@@ -327,14 +392,40 @@ class Launch:
                 params.append(ctypes.c_uint8(int(value)) if kind.kind.value == "uint" else ctypes.c_int8(int(value)))
             else:
                 params.append(c_int(int(value)))
+        dims = (grid.x, grid.y, grid.z)
         blocks = grid.x * grid.y * grid.z
         if blocks == 0:
-            return
-        if program.scratch:
-            scratch = stream.device.empty(D.U8, blocks * program.scratch)
-            params.append(c_void_p(scratch.pointer))
-            stream.note(self.kernel.name, (scratch,))
-        program.launch((grid.x, grid.y, grid.z), hipgen.THREADS, params, stream.handle)
+            return lambda stream: None  # a zero-extent grid launches nothing (reference cuda_backend.py:377-383)
+        if not program.scratch:
+            table = Program.table(params)
+            return lambda stream: program.launch(dims, hipgen.THREADS, table, stream.handle)
+        scratch = StreamScratch(blocks * program.scratch)
+        slot = c_void_p(0)
+        table = Program.table([*params, slot])
+
+        def run(stream: HIPStream) -> None:
+            memory = scratch.on(stream)
+            slot.value = memory.pointer
+            program.launch(dims, hipgen.THREADS, table, stream.handle)
+            stream.note(self.kernel.name, (memory,))
+
+        return run
+
+
+class StreamScratch:
+    """Device scratch of one prepared launch, one buffer per stream it runs on: launches on one stream run in order,
+    so every replay there reuses that stream's buffer, allocated (stream ordered) on its first use. The prepared
+    launch (a `Bound`, a graph) owns it; each launch also holds its buffer until the launch completes."""
+
+    def __init__(self, nbytes: int) -> None:
+        self.nbytes = max(nbytes, 1)
+        self._buffers: dict[int, HIPTensor] = {}
+
+    def on(self, stream: HIPStream) -> HIPTensor:
+        buffer = self._buffers.get(stream.handle)
+        if buffer is None:
+            buffer = self._buffers[stream.handle] = stream.device.empty_on(stream, D.U8, self.nbytes)
+        return buffer
 
 
 def _scalar_value(e: ir.Expr, params: dict) -> np.float32:
@@ -486,8 +577,7 @@ class HIPGraph(Graph):
         except BaseException:  # end the capture and drop its graph, then report the original error
             if hipapi.api().raw("hipStreamEndCapture", handle, ctypes.byref(graph)) == 0 and graph.value:
                 hipapi.api().raw("hipGraphDestroy", graph)
-            stream._pending.clear()
-            stream._keep.clear()
+            stream.take()
             raise
         hipapi.api().hipStreamEndCapture(handle, ctypes.byref(graph))
         executable = c_void_p()
@@ -497,9 +587,7 @@ class HIPGraph(Graph):
             hipapi.api().raw("hipGraphDestroy", graph)
             raise
         # what the recorded launches hold (scratch tensors, arguments) now lives with the graph
-        self._keep = list(stream._keep)
-        stream._pending.clear()
-        stream._keep.clear()
+        self._keep = stream.take()
         weakref.finalize(self, _release_graph, executable.value, graph.value)
         return executable.value
 
@@ -521,6 +609,7 @@ class HIPDevice(Device):
         self.arch, self.ordinal = arch, ordinal
         hipapi.api().hipSetDevice(ordinal)
         library.lib()  # the kernel library must be present: there is no fallback path
+        hipapi.keep_pool(ordinal)
         self._default = HIPStream(self, hipapi.stream_create())
         self._streams: list[HIPStream] = [self._default]
 
@@ -544,10 +633,17 @@ class HIPDevice(Device):
         return self._capture
 
     def empty(self, dtype, *shape: int) -> HIPTensor:
+        """Uninitialized memory, allocated on the launch stream (stream ordered) or, while that stream records a
+        graph, by a plain allocation the graph keeps."""
+        return self.empty_on(self.launch_stream(), dtype, *shape)
+
+    def empty_on(self, stream: HIPStream, dtype, *shape: int) -> HIPTensor:
         element = D.of(dtype)
         count = int(np.prod(shape)) if shape else 1
-        pointer = hipapi.malloc(count * D.NUMPY[element].itemsize)
-        return HIPTensor(self, pointer, element, shape)
+        nbytes = count * D.NUMPY[element].itemsize
+        if stream.capturing:
+            return HIPTensor(self, hipapi.malloc(nbytes), element, shape)
+        return HIPTensor(self, hipapi.malloc_async(nbytes, stream.handle), element, shape, stream=stream)
 
     def to_device(self, array: np.ndarray, dtype=None) -> HIPTensor:
         """A device copy of a host array. bf16 and fp8 arrays pass their element type (`T.bf16`, `T.f8e4m3fn`)."""
@@ -578,13 +674,20 @@ class HIPBackend(Backend):
 
     def __init__(self) -> None:
         self._devices: dict[str, HIPDevice] = {}
+        self._lock = threading.Lock()
 
-    def device(self, arch: str) -> HIPDevice:
+    def device(self, target) -> HIPDevice:
+        """The one device of `target`: krn's `Target` (an AMD target, read by its `arch`; reference
+        src/krn/runtime/api.py:312-354, src/krn/facts/targets.py:214-237) or the arch name itself."""
+        arch = api.arch_of(target)
+        if getattr(target, "vendor", self.vendor) != self.vendor:
+            raise TypeError(f"the amd backend builds devices for AMD targets, not {arch}")
         if arch != TARGET:
             raise api.BackendUnavailable(f"the AMD backend serves {TARGET}, not {arch}")
-        if arch not in self._devices:
-            self._devices[arch] = HIPDevice(arch)
-        return self._devices[arch]
+        with self._lock:
+            if arch not in self._devices:
+                self._devices[arch] = HIPDevice(arch)
+            return self._devices[arch]
 
 
 BACKEND = HIPBackend()

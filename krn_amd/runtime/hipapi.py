@@ -44,6 +44,12 @@ class _Api:
             "hipDeviceGetName": [c_char_p, c_int, c_int],
             "hipMalloc": [POINTER(c_void_p), c_size_t],
             "hipFree": [c_void_p],
+            "hipMemGetInfo": [POINTER(c_size_t), POINTER(c_size_t)],
+            "hipMallocAsync": [POINTER(c_void_p), c_size_t, hipStream_t],
+            "hipFreeAsync": [c_void_p, hipStream_t],
+            "hipDeviceGetDefaultMemPool": [POINTER(c_void_p), c_int],
+            "hipMemPoolSetAttribute": [c_void_p, c_int, c_void_p],
+            "hipStreamIsCapturing": [hipStream_t, POINTER(c_int)],
             "hipHostMalloc": [POINTER(c_void_p), c_size_t, c_uint],
             "hipHostFree": [c_void_p],
             "hipMemcpy": [c_void_p, c_void_p, c_size_t, c_int],
@@ -130,6 +136,45 @@ def malloc(nbytes: int) -> int:
 
 def free(pointer: int) -> None:
     api().hipFree(c_void_p(pointer))
+
+
+def malloc_async(nbytes: int, stream: int) -> int:
+    """Device memory from the device's default pool, ordered on `stream`: usable by work queued after this call on
+    that stream, or on a stream that waited for an event recorded after it."""
+    pointer = c_void_p()
+    api().hipMallocAsync(byref(pointer), max(nbytes, 1), c_void_p(stream))
+    return pointer.value or 0
+
+
+def free_async(pointer: int, stream: int) -> None:
+    """Return memory to its pool once the work queued on `stream` so far has run."""
+    api().hipFreeAsync(c_void_p(pointer), c_void_p(stream))
+
+
+RELEASE_THRESHOLD = 4  # hipMemPoolAttrReleaseThreshold
+
+
+def keep_pool(ordinal: int) -> None:
+    """Let the default pool of a device keep freed memory instead of returning it to the driver at every
+    synchronization, so that stream-ordered allocation of a recently freed size costs no driver allocation."""
+    pool = c_void_p()
+    api().hipDeviceGetDefaultMemPool(byref(pool), ordinal)
+    threshold = ctypes.c_uint64(2**64 - 1)
+    api().hipMemPoolSetAttribute(pool, RELEASE_THRESHOLD, ctypes.cast(byref(threshold), c_void_p))
+
+
+def capturing(stream: int) -> bool:
+    """Is `stream` recording a graph (hipStreamCaptureStatusActive) right now?"""
+    status = c_int(0)
+    api().hipStreamIsCapturing(c_void_p(stream), byref(status))
+    return status.value == 1
+
+
+def memory_free() -> int:
+    """Bytes of device memory the driver reports free (hipMemGetInfo)."""
+    free_bytes, total = c_size_t(), c_size_t()
+    api().hipMemGetInfo(byref(free_bytes), byref(total))
+    return free_bytes.value
 
 
 def stream_create() -> int:

@@ -17,6 +17,7 @@ KINDS = {F32: 0, F16: 1, BF16: 2, F8E4M3: 3, I8: 4, I32: 5}
 # epilogue operations of krn_gemm_nt, applied in order with one float32 rounding each
 MUL_SCALAR, MUL_ROW, MUL_COL, ADD_SCALAR, ADD_ROW, ADD_COL, RELU, GELU, SILU = range(9)
 ACTIVATIONS = {"relu": RELU, "gelu": GELU, "silu": SILU}
+MAX_OPS = 4  # the longest epilogue chain krn_gemm_nt takes (struct Epilogue in krn_amd/csrc/gemm.hip)
 # element kind of a row/column vector, added to the operation code (float32 is 0)
 VECTOR_KINDS = {F32: 0, F16: 16, BF16: 32}
 

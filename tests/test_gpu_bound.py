@@ -57,6 +57,35 @@ def test_bound_nn_product_keeps_its_scratch(device):
         np.testing.assert_array_equal(c.to_host(), want, err_msg=f"replay {replay}")
 
 
+def test_bound_nn_replays_with_event_waits_only_keep_memory_flat(device):
+    """A bound NN product replayed many times on a side stream, waiting only on its own events (never a stream
+    synchronization): the transposed-operand scratch is allocated once per stream and reused, and the stream releases
+    the launches' arguments as their markers complete, so neither device memory nor held launches grow."""
+    from krn_amd.runtime import hipapi
+
+    rng = np.random.default_rng(54)
+    m, n, k = 256, 2048, 2048  # 8 MiB of scratch per transposed operand
+    da = device.to_device(rng.uniform(-1, 1, (m, k)).astype(np.float16))
+    db = device.to_device(rng.uniform(-1, 1, (k, n)).astype(np.float16))
+    c = device.empty(T.f16, m, n)
+    launcher = programs.matmul[programs.Tiling(bm=64, bn=64, bk=32)]
+    launcher(da, db, c)
+    want = c.to_host()
+    side = device.stream()
+    with side:
+        bound = launcher.bind(da, db, c)
+        bound.submit().wait()
+        before = hipapi.memory_free()
+        for _ in range(400):
+            event = bound.submit()
+        event.wait()
+        after = hipapi.memory_free()
+        side.record().wait()
+    assert before - after < 64 << 20, f"device memory fell by {(before - after) >> 20} MiB over 400 replays"
+    assert side.pending_launches() == ()
+    np.testing.assert_array_equal(c.to_host(side), want)
+
+
 def test_bound_attention_and_softmax_match_direct_calls(device):
     rng = np.random.default_rng(53)
     heads, seq, d = 2, 200, 64
