@@ -113,24 +113,23 @@ def softmax_f16(device, steps, warmup, rng, rows=32768, cols=4096):
     return events_ms(stream, run, steps), 2 * 2 * rows * cols
 
 
-def vendor_gemm_bf16(steps, warmup, n=8192):
-    """The same bf16 product through torch.matmul (hipBLASLt): a reference point for the headline, never the
-    product (krn_amd itself does not use torch)."""
-    import torch
+def lib_matmul_bf16(device, steps, warmup, rng, library, n=8192):
+    """krn's `lib.matmul` (C = A @ B with B stored K x N, the reference's NN form) on bf16 8192^3 through one named
+    candidate: "hipblaslt" (the vendor library, the first of the reference's AMD order) or "ours" (krn's
+    matmul_epilogue tile program on the MFMA GEMM)."""
+    from krn_amd import T
+    from krn_amd.lib import lib
 
-    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
-    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    a = device.to_device(bf16_words(rng.standard_normal((n, n), dtype=np.float32)), T.bf16)
+    b = device.to_device(bf16_words(rng.standard_normal((n, n), dtype=np.float32)), T.bf16)
+    c = device.empty(T.bf16, n, n)
+
+    def run():
+        lib.matmul(a, b, out=c, library=library)
+
     for _ in range(warmup):
-        c = a @ b.T
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(steps):
-        c = a @ b.T
-    end.record()
-    torch.cuda.synchronize()
-    del c
-    return start.elapsed_time(end) / steps
+        run()
+    return events_ms(device.default_stream, run, steps)
 
 
 def quantize_e4m3(x: np.ndarray) -> tuple[np.ndarray, np.float32]:
@@ -214,8 +213,8 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--only", default="", help="comma list of extra legs to run (fa, fp8, int8, softmax, copy, "
-                        "blas); copy (the known-size calibration kernel for HBM byte counters) and blas (the same bf16 "
-                        "product through torch/hipBLASLt, a vendor reference point) run only when named")
+                        "blas); copy (the known-size calibration kernel for HBM byte counters) and blas (lib.matmul bf16 "
+                        "8192^3 through the hipBLASLt candidate and through ours) run only when named")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the tile kernels shard by output "
@@ -264,9 +263,11 @@ def main() -> None:
         extra["transpose16_8192x8192"] = {"ms": round(c_ms, 4), "bytes_read": c_bytes, "bytes_written": c_bytes,
                                           "gbps": round(2 * c_bytes / c_ms / 1e6, 1)}
     if "blas" in legs:
-        print("[bench] hipBLASLt bf16 gemm 8192^3 (torch.matmul, reference point)", file=sys.stderr, flush=True)
-        v_ms = vendor_gemm_bf16(args.steps, args.warmup)
-        extra["hipblaslt_bf16_gemm_8192_reference"] = {"ms": round(v_ms, 4), "tflops": round(flops / v_ms / 1e9, 1)}
+        for library in ("hipblaslt", "ours"):
+            print(f"[bench] lib.matmul bf16 8192^3 (NN) through {library}", file=sys.stderr, flush=True)
+            v_ms = lib_matmul_bf16(device, args.steps, args.warmup, rng, library)
+            extra[f"lib_matmul_bf16_nn_8192_{library}"] = {"ms": round(v_ms, 4),
+                                                            "tflops": round(flops / v_ms / 1e9, 1)}
     baseline = None
     if not args.no_cpu:
         print("[bench] CPU baseline (oracle C backend, bounded sample)", file=sys.stderr, flush=True)

@@ -176,12 +176,16 @@ class Capture:
             if isinstance(annotation, ast.Subscript) and base_name in ("Tensor", "Matrix", "Vector", "Tensor3"):
                 items = annotation.slice.elts if isinstance(annotation.slice, ast.Tuple) else [annotation.slice]
                 element = dtype_name(items[0])
-                if element is None or element in ("int", "float", "bool"):
+                generic = element is None and isinstance(items[0], ast.Name)  # `Matrix[F]`, F a type variable
+                if generic and name not in self.dtype_overrides:
+                    raise self.error(arg, f"tensor `{name}` is generic over {items[0].id}: its element type comes from "
+                                          "the argument, and none was given")
+                if not generic and (element is None or element in ("int", "float", "bool")):
                     raise self.error(arg, f"tensor `{name}` needs an element type such as T.f32")
                 rank = TENSOR_RANKS.get(base_name, len(items) - 1)
                 if rank < 1:
                     raise self.error(arg, f"tensor `{name}` needs at least one axis: Tensor[T.f32, int, int]")
-                dtype = self.dtype_overrides.get(name, D.BY_NAME[element])
+                dtype = self.dtype_overrides[name] if generic else self.dtype_overrides.get(name, D.BY_NAME[element])
                 kind = TensorType(dtype, rank)
                 self.params.append((name, kind))
                 self.env[name] = TensorRef(name, kind)

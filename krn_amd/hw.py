@@ -3,7 +3,8 @@
 Mirrors `krn.hw.Libraries` (reference src/krn/hw/libraries.py:324-377): `load(name)` returns a frozen record with the
 path and the ctypes handle, `find(name)` only locates, `available(name)` checks loading, and a failure raises
 `LibraryNotFound` naming where it looked. The reference has a `"hip"` spec (libraries.py:85-90) and no hiprtc spec;
-this module adds `"hiprtc"`, `"krn_amd"` (the in-tree `libkrn_amd.so`) and `"roctx"` (the reference's ROCTx loader,
+this module adds `"hiprtc"`, `"hipblaslt"` (the vendor GEMM behind `lib.matmul`'s first AMD candidate, reference
+src/krn/lib/lib.py:264 and 516), `"krn_amd"` (the in-tree `libkrn_amd.so`) and `"roctx"` (the reference's ROCTx loader,
 src/krn/profile/providers/amd/tracer.py:13-28).
 """
 
@@ -19,12 +20,14 @@ FILENAMES = {
     "hip": ("libamdhip64.so", "libamdhip64.so.7"),
     "hiprtc": ("libhiprtc.so", "libhiprtc.so.7"),
     "krn_amd": ("libkrn_amd.so",),
+    "hipblaslt": ("libhipblaslt.so", "libhipblaslt.so.1"),
     # rocprofv3 (rocprofiler-sdk) records ranges from its own ROCTx library; the older roctracer one is the fallback
     "roctx": ("librocprofiler-sdk-roctx.so", "librocprofiler-sdk-roctx.so.1", "libroctx64.so", "libroctx64.so.4"),
 }
 FIXES = {
     "hip": "Install ROCm (libamdhip64.so under /opt/rocm/lib)",
     "hiprtc": "Install ROCm (libhiprtc.so under /opt/rocm/lib)",
+    "hipblaslt": "Install ROCm's hipBLASLt (libhipblaslt.so under /opt/rocm/lib)",
     "krn_amd": "Build the gfx950 kernels first: python -c 'import __graft_entry__ as g; g.build()'",
     "roctx": "Install ROCm's ROCTx library (librocprofiler-sdk-roctx.so under /opt/rocm/lib)",
 }

@@ -46,6 +46,25 @@ def test_elementwise_tile_programs_match_the_c_oracle(device, name, size):
 
 
 @pytest.mark.parametrize("size", SIZES)
+def test_elementwise_tile_programs_match_numpy(device, size):
+    """The same programs against expectations written out in numpy (reference tests/frontend/test_tile_ops.py:54-118,
+    212-213), so a capture mistake shared by the device path and the oracle cannot pass: rows and columns past the
+    tensor's edge are invalid lanes and are neither read nor stored."""
+    rng = np.random.default_rng(100 + sum(size))
+    x = rng.standard_normal(size).astype(np.float32)
+    keep = np.arange(size[1])[None, :] <= np.arange(size[0])[:, None]
+    expected = {
+        "transpose": x.T,
+        "select": np.where(x > 0, x, np.float32(0.5)),
+        "causal": np.where(keep, x, np.float32(-1.0e30)),
+        "scaled_by_extent": x * np.float32(programs.Shape().cols),  # the tile's extent, not the valid width
+    }
+    for name, want in expected.items():
+        out = np.full(want.shape, -7.0, np.float32)
+        np.testing.assert_array_equal(on_gpu(device, name, [x, out])[1], want, err_msg=name)
+
+
+@pytest.mark.parametrize("size", SIZES)
 def test_comparisons_and_positions_are_exact(device, size):
     rng = np.random.default_rng(5)
     x = np.round(rng.standard_normal(size)).astype(np.float32)

@@ -74,6 +74,21 @@ def test_f32_lib_matmul_matches_the_c_oracle(device, name):
     got = out.to_host()
     want, bound = reference(a, b, bias, flags)
     assert np.all(np.abs(got.astype(np.float64) - want) <= bound)
+    # written out in float32 numpy as well, so the check does not rest on the captured program: one fused
+    # multiply-add per k in k order, then the bias add and the activation each rounded to float32
+    acc = np.zeros((m, n), np.float32)
+    for kk in range(k):
+        acc = (acc.astype(np.float64) + a[:, kk:kk + 1].astype(np.float64) * b[kk:kk + 1, :]).astype(np.float32)
+    if flags.get("bias"):
+        acc = acc + bias
+    exact = {"relu": lambda x: np.where(x < 0, np.float32(0), x),
+             "gelu": lambda x: (np.float32(0.5) * x * (np.float32(1) + ERF(x / np.float32(math.sqrt(2)))
+                                                        .astype(np.float32))).astype(np.float32),
+             "silu": lambda x: (x / (np.float32(1) + np.exp(-x))).astype(np.float32)}
+    for flag, fn in exact.items():
+        if flags.get(flag):
+            acc = fn(acc)
+    np.testing.assert_allclose(got, acc, rtol=8 * 2.0**-23, atol=2.0**-20)
     from krn_amd.compiler.capture import capture
 
     oracle = np.zeros((m, n), np.float32)
