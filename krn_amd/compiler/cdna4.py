@@ -304,3 +304,18 @@ def lower(kernel: ir.Kernel) -> GemmPlan | AttentionPlan | SoftmaxPlan | Generic
     """The plan for `kernel` on gfx950: a hand-written kernel when the program is one they serve, otherwise the
     generic HIP lowering."""
     return match_gemm(kernel) or match_attention(kernel) or match_softmax(kernel) or GenericPlan(kernel)
+
+
+def why_generic(kernel: ir.Kernel) -> list[str]:
+    """Why no hand-written kernel serves `kernel`: one line per specialised plan it did not match."""
+    reasons = []
+    if match_gemm(kernel) is None:
+        reasons.append("not the whole-product GEMM: `acc = zeros`, one K loop `acc += a[rows, ks] @ b[cols, ks]"
+                       ".transpose()` (or `b[ks, cols]`) of bf16/f16/fp8/int8 operands, one store of an epilogue of "
+                       "scalar or row/column vector mul/add and relu/gelu/silu")
+    if match_attention(kernel) is None:
+        reasons.append("not krn's flash-attention program with head dimension 64 or 128 and f16/bf16 (compared with "
+                       "the canonical program's IR)")
+    if match_softmax(kernel) is None:
+        reasons.append("not one of krn's row-softmax programs (compared with the canonical programs' IR)")
+    return reasons

@@ -12,6 +12,7 @@ skip invalid lanes and elements outside the tensor. The kernel ABI is krn's gene
 """
 
 import math
+from dataclasses import dataclass
 
 from krn_amd.compiler import ir
 from krn_amd.dtypes import BF16, BOOL, F16, F32, F64, I8, I32, I64, PY_FLOAT, PY_INT, Dtype, Kind
@@ -47,6 +48,10 @@ SIZES = {"unsigned char": 1, "signed char": 1, "_Float16": 2, "short": 2, "unsig
 
 PRELUDE = r"""
 typedef unsigned int u32;
+typedef _Float16 _k_half4 __attribute__((ext_vector_type(4)));
+typedef short _k_short4 __attribute__((ext_vector_type(4)));
+typedef float _k_float4 __attribute__((ext_vector_type(4)));
+typedef int _k_int4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float kb16(float x) {
   u32 u = __float_as_uint(x);
   if ((u & 0x7fffffffu) > 0x7f800000u) u = (u | 0x400000u) & 0xffff0000u;
@@ -90,9 +95,62 @@ MATH = {
 }  # fmt: skip
 
 
+@dataclass(frozen=True)
+class MfmaForm:
+    """A 16 x 16 x K_STEP matrix-core instruction the generic lowering uses for a product."""
+
+    name: str
+    builtin: str
+    k_step: int
+    element: str  # the staged operand element
+    operand_vec: str  # one lane's operand of one instruction
+    acc_vec: str
+    integer: bool = False
+
+
+MFMA_FORMS = {
+    F16: MfmaForm("f16", "__builtin_amdgcn_mfma_f32_16x16x16f16", 16, "unsigned short", "_k_half4", "_k_float4"),
+    BF16: MfmaForm("bf16", "__builtin_amdgcn_mfma_f32_16x16x16bf16_1k", 16, "unsigned short", "_k_short4",
+                   "_k_float4"),
+    I8: MfmaForm("i8", "__builtin_amdgcn_mfma_i32_16x16x32_i8", 32, "signed char", "long", "_k_int4", True),
+}
+
+
+def mfma_form(s: ir.Accumulate) -> MfmaForm | None:
+    """The matrix-core instruction for a product, when its operand types have one and the tile extents are whole
+    instructions (m and n multiples of 16, k of the instruction's K); None keeps the scalar fused multiply-adds.
+    f16/bf16 products accumulate in float32, int8 ones in int32 (exact, so any order gives the same result)."""
+    (m, k), n = s.lhs.shape, s.rhs.shape[1]
+    if s.lhs.dtype != s.rhs.dtype or s.lhs.dtype not in MFMA_FORMS:
+        return None
+    form = MFMA_FORMS[s.lhs.dtype]
+    if (s.acc.dtype == I32) != form.integer or (not form.integer and s.acc.dtype != F32):
+        return None
+    if m % 16 or n % 16 or k % form.k_step:
+        return None
+    return form
+
+
+def products(kernel: ir.Kernel) -> list[str]:
+    """How the generic lowering runs each product of `kernel`: "mfma 16x16x<K> <type>" or "scalar fma"."""
+    found: list[str] = []
+
+    def walk(statements) -> None:
+        for s in statements:
+            if isinstance(s, ir.Accumulate):
+                form = mfma_form(s)
+                found.append(f"mfma 16x16x{form.k_step} {form.name}" if form else "scalar fma")
+            for field_name in ("body", "then", "orelse"):
+                walk(getattr(s, field_name, ()) or ())
+
+    walk(kernel.body)
+    return found
+
+
 class Emitter:
     def __init__(self, kernel: ir.Kernel, entry: str) -> None:
         self.kernel, self.entry = kernel, entry
+        self.mfma_products = 0
         self.lines: list[str] = []
         self.buffers: list[tuple[str, str, int]] = []
         self.depth = 1
@@ -204,6 +262,10 @@ class Emitter:
         stage = "int" if integer else "float"
         a, av = self.tile(s.lhs)
         b, bv = self.tile(s.rhs)
+        form = mfma_form(s)
+        if form is not None:
+            self.mfma_product(s, form, (a, av), (b, bv), (acc, acc_v))
+            return
         af, bf = self.staged(stage, a, av, s.lhs), self.staged(stage, b, bv, s.rhs)
         self.put(f"for (int _e = threadIdx.x; _e < {m * n}; _e += {THREADS}) {{")
         self.put(f"  const int _i = _e / {n}, _j = _e % {n};")
@@ -220,6 +282,61 @@ class Emitter:
         self.put(f"  {acc_v}[_e] = {acc_v}[_e] & _row & _col;")
         self.put("}")
         self.put("__syncthreads();")
+
+    def mfma_product(self, s: ir.Accumulate, form: "MfmaForm", lhs, rhs, accumulator) -> None:
+        """acc[m, n] += lhs[m, k] @ rhs[k, n] on the matrix cores: both operands staged into LDS K-contiguous as the
+        instruction's operand type (invalid lanes 0, so they add nothing), then each of the 4 waves takes 16 x 16
+        output blocks in turn, loads the block's accumulators, runs k / K_STEP MFMAs and writes them back. Lane l of
+        a 16x16xK MFMA holds operand row (or column) l % 16 and K_STEP / 4 consecutive k from (l / 16) * K_STEP / 4,
+        and accumulators rows 4 (l / 16) + i, column l % 16 (reference compiler/hip.py:70-97 `AMDMFMA.product`,
+        compiler/emit.py:924-955 `matrix_stage`). The validity of the accumulator is the scalar path's."""
+        (a, av), (b, bv), (acc, acc_v) = lhs, rhs, accumulator
+        (m, k), n = s.lhs.shape, s.rhs.shape[1]
+        per = form.k_step // 4  # operand elements per lane per instruction
+        at = self.mfma_stage(form, a, av, s.lhs, m, k, transposed=False)
+        bt = self.mfma_stage(form, b, bv, s.rhs, n, k, transposed=True)
+        acc_t = "int" if form.integer else "float"
+        self.put("{")
+        self.put("  const int _w = threadIdx.x >> 6, _l = threadIdx.x & 63, _r = _l & 15, _q = _l >> 4;")
+        self.put(f"  for (int _blk = _w; _blk < {(m // 16) * (n // 16)}; _blk += {THREADS // 64}) {{")
+        self.put(f"    const int _m0 = (_blk / {n // 16}) * 16, _n0 = (_blk % {n // 16}) * 16;")
+        self.put(f"    {form.acc_vec} _c;")
+        self.put(f"    for (int _i = 0; _i < 4; ++_i) _c[_i] = {acc}[(_m0 + 4 * _q + _i) * {n} + _n0 + _r];")
+        self.put(f"    for (int _k = 0; _k < {k}; _k += {form.k_step}) {{")
+        self.put(f"      const {form.operand_vec} _a = *(const {form.operand_vec}*)&{at}[(_m0 + _r) * {k} + _k + _q * {per}];")
+        self.put(f"      const {form.operand_vec} _b = *(const {form.operand_vec}*)&{bt}[(_n0 + _r) * {k} + _k + _q * {per}];")
+        self.put(f"      _c = {form.builtin}(_a, _b, _c, 0, 0, 0);")
+        self.put("    }")
+        self.put(f"    for (int _i = 0; _i < 4; ++_i) {acc}[(_m0 + 4 * _q + _i) * {n} + _n0 + _r] = ({acc_t})_c[_i];")
+        self.put("  }")
+        self.put("}")
+        self.put(f"for (int _e = threadIdx.x; _e < {m * n}; _e += {THREADS}) {{")
+        self.put(f"  const int _i = _e / {n}, _j = _e % {n};")
+        self.put(f"  unsigned char _row = 0, _col = 0;")
+        self.put(f"  for (int _k = 0; _k < {k}; ++_k) {{ _row |= {av}[_i * {k} + _k]; _col |= {bv}[_k * {n} + _j]; }}")
+        self.put(f"  {acc_v}[_e] = {acc_v}[_e] & _row & _col;")
+        self.put("}")
+        self.put("__syncthreads();")
+        self.mfma_products += 1
+
+    def mfma_stage(self, form: "MfmaForm", value: str, valid: str, e: ir.Expr, rows: int, k: int,
+                   transposed: bool) -> str:
+        """An operand in LDS as `rows` K-contiguous rows of the instruction's element bits; `transposed` reads a
+        (k, rows) tile."""
+        self.count += 1
+        name = f"mf{self.count}"
+        self.buffers.append((name, form.element, rows * k))
+        source = f"{value}[_kk * {rows} + _rr]" if transposed else f"{value}[_rr * {k} + _kk]"
+        check = f"{valid}[_kk * {rows} + _rr]" if transposed else f"{valid}[_rr * {k} + _kk]"
+        bits = {"f16": f"__builtin_bit_cast(unsigned short, (_Float16){source})",
+                "bf16": f"(unsigned short)(__float_as_uint({source}) >> 16)",
+                "i8": f"(signed char){source}"}[form.name]
+        self.put(f"for (int _e = threadIdx.x; _e < {rows * k}; _e += {THREADS}) {{")
+        self.put(f"  const int _rr = _e / {k}, _kk = _e % {k};")
+        self.put(f"  {name}[_e] = {check} ? {bits} : ({form.element})0;")
+        self.put("}")
+        self.put("__syncthreads();")
+        return name
 
     def staged(self, stage: str, value: str, valid: str, e: ir.Expr) -> str:
         self.count += 1

@@ -282,19 +282,12 @@ class Launch:
     def prepare(self, values: list[object], grid: Blocks) -> Callable[[HIPStream], None]:
         """The launch of these argument values on this grid as one call per stream: the plan's checks and argument
         marshalling run here, once, so a `Bound` replays only the library call."""
-        params = dict(zip((name for name, _ in self.kernel.params), values))
-        plan = self.plan
-        call = None
-        if isinstance(plan, cdna4.GemmPlan):
-            call = self._gemm(plan, params, grid)
-        elif isinstance(plan, cdna4.AttentionPlan):
-            call = self._attention(plan, params, grid)
-        elif isinstance(plan, cdna4.SoftmaxPlan):
-            call = self._softmax(plan, params, grid)
+        call = self.specialised(values, grid)
+        route = type(self.plan).__name__
         if call is None:
-            call = self._generic(values, grid)
+            call, route = self._generic(values, grid), "GenericPlan"
 
-        name = f"krn:{self.kernel.name} {type(plan).__name__}"
+        name = f"krn:{self.kernel.name} {route}"
 
         def run(stream: HIPStream) -> None:
             if not roctx.launch_ranges():
@@ -307,6 +300,19 @@ class Launch:
 
     def run(self, values: list[object], grid: Blocks, stream: HIPStream) -> None:
         self.prepare(values, grid)(stream)
+
+    def specialised(self, values: list[object], grid: Blocks) -> Callable[[HIPStream], None] | None:
+        """The hand-written kernel's call when the plan is one and these arguments and this grid are the whole
+        problem it computes; None sends the launch to the generic lowering, which keeps the program's meaning."""
+        params = dict(zip((name for name, _ in self.kernel.params), values))
+        plan = self.plan
+        if isinstance(plan, cdna4.GemmPlan):
+            return self._gemm(plan, params, grid)
+        if isinstance(plan, cdna4.AttentionPlan):
+            return self._attention(plan, params, grid)
+        if isinstance(plan, cdna4.SoftmaxPlan):
+            return self._softmax(plan, params, grid)
+        return None
 
     def _gemm(self, plan: cdna4.GemmPlan, params: dict, grid: Blocks):
         a, b, c = params[plan.a], params[plan.b], params[plan.c]
@@ -510,9 +516,22 @@ class HIPLauncher(Launcher):
         return HIPBound(self, self.ordered(args, kwargs))
 
     def explain(self, *args, **kwargs) -> dict:
-        launch = self.plan(self.ordered(args, kwargs))
-        return {"kernel": launch.kernel.name, "target": TARGET, "plan": type(launch.plan).__name__,
-                "detail": repr(launch.plan) if not isinstance(launch.plan, cdna4.GenericPlan) else "hipgen"}
+        """What a launch with these arguments runs: the plan that serves it and, for the generic lowering, why no
+        hand-written kernel took it and how each product runs ("mfma 16x16x16 bf16" or "scalar fma")."""
+        args = self.ordered(args, kwargs)
+        launch = self.plan(args)
+        values = space.runtime_args(launch.kernel, args)
+        grid = self.launch if self.launch is not None else space.geometry(launch.kernel, values)
+        if launch.specialised(values, grid) is not None:
+            return {"kernel": launch.kernel.name, "target": TARGET, "plan": type(launch.plan).__name__,
+                    "detail": repr(launch.plan)}
+        if isinstance(launch.plan, cdna4.GenericPlan):
+            why = cdna4.why_generic(launch.kernel)
+        else:
+            why = [f"the program is a {type(launch.plan).__name__}, but these arguments or this grid are not the whole "
+                   "problem its kernel computes (the grid must cover the output once, the loop the whole extent)"]
+        return {"kernel": launch.kernel.name, "target": TARGET, "plan": "GenericPlan", "detail": "hipgen",
+                "products": hipgen.products(launch.kernel), "why": why}
 
 
 class HIPBound(Bound):

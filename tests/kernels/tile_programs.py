@@ -348,3 +348,31 @@ def softmax_bf16(x: Matrix[T.bf16], y: Matrix[T.bf16], t: RowTiling) -> None:
 def softmax_f32(x: Matrix[T.f32], y: Matrix[T.f32], t: RowTiling) -> None:
     rows, cols = block.tile(t.rows), slice(0, t.cols)
     y[rows, cols] = x[rows, cols].to(T.f32).softmax(axis=1).to(T.f32)
+
+
+@struct
+class PartialK:
+    bm: Const[int] = 64
+    bn: Const[int] = 64
+    bk: Const[int] = 32
+    kk: Const[int] = 96
+
+
+@kernel
+def gemm_partial_k(t: PartialK, a: Matrix[T.bf16], b: Matrix[T.bf16], c: Matrix[T.f32]) -> None:
+    """The product over the first t.kk columns of K only: not the whole product, so the generic lowering runs it,
+    its products on the matrix cores."""
+    rows, cols = block.tile(t.bm, t.bn)
+    acc = zeros(T.f32, t.bm, t.bn)
+    for ks in pipelined(t.kk, t.bk):
+        acc += a[rows, ks] @ b[cols, ks].transpose()
+    c[rows, cols] = acc
+
+
+@kernel
+def gemm_i8_partial_k(t: PartialK, a: Matrix[T.i8], b: Matrix[T.i8], c: Matrix[T.i32]) -> None:
+    rows, cols = block.tile(t.bm, t.bn)
+    acc = zeros(T.i32, t.bm, t.bn)
+    for ks in pipelined(t.kk, t.bk):
+        acc += a[rows, ks] @ b[cols, ks].transpose()
+    c[rows, cols] = acc

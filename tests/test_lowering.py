@@ -128,3 +128,38 @@ def test_gemm_launch_marshals_once_and_refuses_partial_grids(monkeypatch):
         run(SimpleNamespace(handle=9))
     assert ran == [9, 9, 9] and len(made) == 1
     assert launch._gemm(plan, params, Blocks(3, 1)) is None
+
+
+@pytest.mark.parametrize("name, consts, products", [
+    ("gemm_partial_k", {"bm": 64, "bn": 64, "bk": 32, "kk": 96}, ["mfma 16x16x16 bf16"]),
+    ("gemm_i8_partial_k", {"bm": 64, "bn": 64, "bk": 64, "kk": 128}, ["mfma 16x16x32 i8"]),
+    ("flash_attention_bf16", {"bq": 64, "bk": 64, "d": 32, "causal": True}, ["mfma 16x16x16 bf16"] * 2),
+    ("flash_attention", {"bq": 8, "bk": 8, "d": 16, "causal": True}, ["scalar fma"] * 2),
+    ("product", {"rows": 8, "cols": 16}, ["scalar fma"]),
+])  # fmt: skip
+def test_generic_products_take_the_matrix_cores_when_the_tile_extents_allow(name, consts, products):
+    """m and n multiples of 16 and k of the instruction's K: a 16x16x16 f16/bf16 or 16x16x32 i8 MFMA; otherwise the
+    scalar fused multiply-adds in k order."""
+    from krn_amd.compiler import hipgen
+
+    kernel = capture(KERNELS, name, consts={"t": consts})
+    assert hipgen.products(kernel) == products
+    source, _ = hipgen.emit(kernel, "krn_probe")
+    assert ("__builtin_amdgcn_mfma" in source) == any(p.startswith("mfma") for p in products)
+
+
+def test_the_generic_mfma_source_compiles_for_gfx950(tmp_path):
+    """The generated products compile for gfx950 (hipcc cross-compiles here; the GPU tests run them)."""
+    import shutil
+    import subprocess
+
+    from krn_amd.compiler import hipgen
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    kernel = capture(KERNELS, "gemm_i8_partial_k", consts={"t": {"bm": 64, "bn": 64, "bk": 64, "kk": 128}})
+    source, _ = hipgen.emit(kernel, "krn_probe")
+    path = tmp_path / "probe.hip"
+    path.write_text("#include <hip/hip_runtime.h>\n" + source)
+    result = subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-c", str(path), "-o", str(tmp_path / "p.o")],
+                            capture_output=True, text=True)
+    assert result.returncode == 0, result.stderr[-2000:]
