@@ -48,6 +48,19 @@ enum krn_epilogue_op {
 int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n, int64_t k,
                 int nops, const int* ops, const float* scalars, const void* const* vectors, void* stream);
 
+/* C[m, n] = epilogue(sum_k A[m, k] * B[k, n]), A: M x K, B: K x N (the NN form), C: M x N, bf16 or f16 operands;
+ * out_kind and the epilogue as for krn_gemm_nt. Replaces krn's own GEMM tile program `acc += a[rows, ks] @
+ * b[ks, cols]` (reference examples/04_libraries/01_gemm_tiles.py:34-40) and the multiply of lib.matmul
+ * (src/krn/lib/lib_kernels.py:31-48), whose B operand is K x N. B is transposed into `workspace` (at least
+ * krn_gemm_nn_workspace(n, k) bytes of device memory, owned by the caller) and the NT kernels run on it; the
+ * workspace must not be touched by other work until this call's work on `stream` has run. */
+int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n, int64_t k,
+                int nops, const int* ops, const float* scalars, const void* const* vectors, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace krn_gemm_nn needs for an N-column, K-row B operand (n * k 16-bit elements). */
+int64_t krn_gemm_nn_workspace(int64_t n, int64_t k);
+
 /* out (cols x rows) = in (rows x cols) transposed, 16-bit elements: turns the B operand of `a[rows, ks] @ b[ks, cols]`
  * (reference examples/04_libraries/01_gemm_tiles.py:34-40) K-contiguous for krn_gemm_nt. */
 int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream);

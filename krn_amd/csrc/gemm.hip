@@ -1117,6 +1117,8 @@ static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t
   return -1;
 }
 
+extern "C" int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream);
+
 extern "C" {
 
 // See include/krn_amd.h for the contract of each entry point.
@@ -1185,6 +1187,40 @@ __global__ __launch_bounds__(256) void transpose16(const uint16_t* __restrict__ 
     const int64_t c = c0 + i, r = r0 + tx;
     if (c < cols && r < rows) out[c * rows + r] = tile[tx][i];
   }
+}
+
+// The NN product `a[rows, ks] @ b[ks, cols]` with B stored K x N: B is transposed into `bt` (N x K, n * k 16-bit
+// elements) and the NT kernels run on it. Both launches go on `stream`, in that order.
+static int gemm_nn_through(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n,
+                           int64_t k, int nops, const int* ops, const float* scalars, const void* const* vectors,
+                           void* bt, void* stream) {
+  if (in_kind != BF16 && in_kind != F16) {
+    krn_set_error("gemm_nn: operand kind %d; the NN product takes bf16 or f16 operands", in_kind);
+    return -1;
+  }
+  if (m < 0 || n < 0 || k < 0) {
+    krn_set_error("gemm_nn: negative extent");
+    return -1;
+  }
+  if (n > 0 && k > 0) {
+    const int rc = krn_transpose16(b, bt, k, n, stream);
+    if (rc) return rc;
+  }
+  return krn_gemm_nt(in_kind, a, bt, c, out_kind, m, n, k, nops, ops, scalars, vectors, stream);
+}
+
+extern "C" int64_t krn_gemm_nn_workspace(int64_t n, int64_t k) { return n < 0 || k < 0 ? 0 : n * k * 2; }
+
+extern "C" int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n,
+                           int64_t k, int nops, const int* ops, const float* scalars, const void* const* vectors,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  const int64_t need = krn_gemm_nn_workspace(n, k);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    krn_set_error("gemm_nn: the workspace holds %lld bytes, the transposed operand needs %lld",
+                  (long long)workspace_bytes, (long long)need);
+    return -1;
+  }
+  return gemm_nn_through(in_kind, a, b, c, out_kind, m, n, k, nops, ops, scalars, vectors, workspace, stream);
 }
 
 extern "C" int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream) {

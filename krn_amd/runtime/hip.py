@@ -341,19 +341,19 @@ class Launch:
                 code = base + (1 if op.axis == "row" else 2) + library.VECTOR_KINDS[vector.dtype]
                 ops.append((code, 0.0, vector.pointer))
         if plan.layout == "nn":
-            scratch = StreamScratch(n * k * 2)
-
-            products: dict[int, Callable[[int], None]] = {}  # scratch pointer -> the product marshalled for it
+            need = library.gemm_nn_workspace(n, k)
+            scratch = StreamScratch(need)
+            products: dict[int, Callable[[int], None]] = {}  # workspace pointer -> the product marshalled for it
 
             def nn(stream: HIPStream) -> None:
-                bt = scratch.on(stream)
-                product = products.get(bt.pointer)
+                workspace = scratch.on(stream)
+                product = products.get(workspace.pointer)
                 if product is None:
-                    product = products[bt.pointer] = library.gemm_nt_call(plan.operand, a.pointer, bt.pointer,
-                                                                          c.pointer, plan.output, m, n, k, ops)
-                library.transpose16(b.pointer, bt.pointer, k, n, stream.handle)
+                    product = products[workspace.pointer] = library.gemm_nn_call(
+                        plan.operand, a.pointer, b.pointer, c.pointer, plan.output, m, n, k, ops, workspace.pointer,
+                        max(need, 1))
                 product(stream.handle)
-                stream.note(self.kernel.name, (bt,))
+                stream.note(self.kernel.name, (workspace,))
 
             return nn
         product = library.gemm_nt_call(plan.operand, a.pointer, b.pointer, c.pointer, plan.output, m, n, k, ops)

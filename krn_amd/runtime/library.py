@@ -40,6 +40,13 @@ def lib() -> ctypes.CDLL:
     handle.krn_attention_fwd.argtypes = [
         c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_float, c_int, c_void_p,
     ]  # fmt: skip
+    handle.krn_gemm_nn.restype = c_int
+    handle.krn_gemm_nn.argtypes = [
+        c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64, c_int, POINTER(c_int),
+        POINTER(c_float), POINTER(c_void_p), c_void_p, c_int64, c_void_p,
+    ]  # fmt: skip
+    handle.krn_gemm_nn_workspace.restype = c_int64
+    handle.krn_gemm_nn_workspace.argtypes = [c_int64, c_int64]
     handle.krn_transpose16.restype = c_int
     handle.krn_transpose16.argtypes = [c_void_p, c_void_p, c_int64, c_int64, c_void_p]
     handle.krn_softmax_rows.restype = c_int
@@ -71,6 +78,28 @@ def gemm_nt_call(in_dtype: Dtype, a: int, b: int, c: int, out_dtype: Dtype, m: i
 
     def call(stream: int) -> None:
         check(entry(*head, stream), "krn_gemm_nt")
+
+    return call
+
+
+def gemm_nn_workspace(n: int, k: int) -> int:
+    """Bytes of device workspace krn_gemm_nn needs for a K x N operand B."""
+    return lib().krn_gemm_nn_workspace(n, k)
+
+
+def gemm_nn_call(in_dtype: Dtype, a: int, b: int, c: int, out_dtype: Dtype, m: int, n: int, k: int,
+                 ops: list[tuple[int, float, int]], workspace: int, workspace_bytes: int):
+    """`gemm_nn` (B stored K x N, transposed into `workspace`) as a function of the stream, marshalled once."""
+    count = len(ops)
+    codes = (c_int * max(count, 1))(*(op for op, _, _ in ops))
+    scalars = (c_float * max(count, 1))(*(s for _, s, _ in ops))
+    vectors = (c_void_p * max(count, 1))(*(v for _, _, v in ops))
+    entry = lib().krn_gemm_nn
+    head = (kind(in_dtype), a, b, c, kind(out_dtype), m, n, k, count, codes, scalars, vectors, workspace,
+            workspace_bytes)
+
+    def call(stream: int) -> None:
+        check(entry(*head, stream), "krn_gemm_nn")
 
     return call
 

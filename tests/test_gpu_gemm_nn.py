@@ -1,0 +1,58 @@
+"""krn_gemm_nn, the NN product of krn's own GEMM example (reference examples/04_libraries/01_gemm_tiles.py:34-40,
+B stored K x N), through the C ABI: it transposes B into the caller's workspace and runs the NT kernels, so its
+result is bit-identical to krn_gemm_nt on B transposed on the host; a workspace that is too small is refused before
+anything is enqueued."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from krn_amd import T
+from krn_amd.dtypes import BF16, F16
+from krn_amd.runtime import library
+from oracle.numerics import bf16_words
+
+pytestmark = pytest.mark.gpu
+
+
+def nt(device, dtype, a, bt, m, n, k, out):
+    library.gemm_nt(dtype, a.pointer, bt.pointer, out.pointer, dtype, m, n, k, [], device.default_stream.handle)
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("m,n,k", [(256, 512, 384), (100, 130, 72), (8, 1000, 256), (1024, 1024, 1024)])
+def test_gemm_nn_equals_gemm_nt_on_the_transposed_operand(device, dtype, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    x, y = rng.standard_normal((m, k)).astype(np.float32), rng.standard_normal((k, n)).astype(np.float32)
+    if dtype == BF16:
+        ah, bh, kind = bf16_words(x), bf16_words(y), T.bf16
+    else:
+        ah, bh, kind = x.astype(np.float16), y.astype(np.float16), T.f16
+    a, b = device.to_device(ah, kind), device.to_device(bh, kind)
+    bt = device.to_device(np.ascontiguousarray(bh.T), kind)
+    c_nn, c_nt = device.empty(kind, m, n), device.empty(kind, m, n)
+    need = library.gemm_nn_workspace(n, k)
+    assert need == n * k * 2
+    workspace = device.empty(T.u8, need)
+    stream = device.default_stream.handle
+    library.check(library.lib().krn_gemm_nn(library.kind(dtype), a.pointer, b.pointer, c_nn.pointer,
+                                            library.kind(dtype), m, n, k, 0, None, None, None, workspace.pointer,
+                                            need, stream), "krn_gemm_nn")
+    nt(device, dtype, a, bt, m, n, k, c_nt)
+    np.testing.assert_array_equal(c_nn.to_host(), c_nt.to_host())
+
+
+def test_gemm_nn_refuses_a_small_workspace_and_other_kinds(device):
+    m = n = k = 64
+    a, b = device.empty(T.bf16, m, k), device.empty(T.bf16, k, n)
+    c, workspace = device.empty(T.bf16, m, n), device.empty(T.u8, n * k * 2)
+    call = library.lib().krn_gemm_nn
+    assert call(library.kind(BF16), a.pointer, b.pointer, c.pointer, library.kind(BF16), m, n, k, 0, None, None, None,
+                workspace.pointer, n * k * 2 - 1, None) != 0
+    assert b"workspace" in library.lib().krn_amd_last_error()
+    assert call(library.kind(BF16), a.pointer, b.pointer, c.pointer, library.kind(BF16), m, n, k, 0, None, None, None,
+                None, 0, None) != 0
+    assert call(3, a.pointer, b.pointer, c.pointer, library.kind(BF16), m, n, k, 0, None, None, None,
+                workspace.pointer, n * k * 2, None) != 0  # fp8 operands: not an NN product
+    assert b"bf16 or f16" in library.lib().krn_amd_last_error()
