@@ -61,6 +61,21 @@ int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, int out_kind
 /* Bytes of workspace krn_gemm_nn needs for an N-column, K-row B operand (n * k 16-bit elements). */
 int64_t krn_gemm_nn_workspace(int64_t n, int64_t k);
 
+/* krn_gemm_nn without a workspace and without any allocation: the transposed B operand goes to a device array the
+ * library holds (64 MiB per GPU it runs on, kept until the process ends; krn_gemm_nn_noalloc_limit() returns the
+ * size). This entry point has no counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc,
+ * hipFree or allocating library routine; it refuses a B whose n * k * 2 bytes exceed the limit. The array is looked
+ * up once per device (hipGetSymbolAddress) on that device's first call, with the stream's device current. Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (concurrent streams, or another host thread)
+ * race and must be ordered by the caller. */
+int krn_gemm_nn_noalloc(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n,
+                        int64_t k, int nops, const int* ops, const float* scalars, const void* const* vectors,
+                        void* stream);
+
+/* Bytes of device scratch krn_gemm_nn_noalloc holds per GPU. */
+int64_t krn_gemm_nn_noalloc_limit(void);
+
 /* out (cols x rows) = in (rows x cols) transposed, 16-bit elements: turns the B operand of `a[rows, ks] @ b[ks, cols]`
  * (reference examples/04_libraries/01_gemm_tiles.py:34-40) K-contiguous for krn_gemm_nt. */
 int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream);

@@ -18,6 +18,7 @@
 //
 // LDS layout: a tile row of a K slice is 64 or 128 bytes (4 or 8 chunks of 16 bytes), swizzled per row so that
 // the 16-byte fragment reads of 16 consecutive rows hit distinct banks (swz4 / swz8 below).
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1221,6 +1222,54 @@ extern "C" int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, i
     return -1;
   }
   return gemm_nn_through(in_kind, a, b, c, out_kind, m, n, k, nops, ops, scalars, vectors, workspace, stream);
+}
+
+// The scratch of krn_gemm_nn_noalloc: the transposed B operand lives in this file-scope device array instead of a
+// caller's workspace or an allocation. Every GPU the library runs on holds its own copy until the process ends. In
+// host code `scratch` names a host-side stand-in, not the device memory: the device address comes from
+// hipGetSymbolAddress, once per device, and only that address is handed to kernels.
+constexpr int64_t KRN_NN_SCRATCH_BYTES = (int64_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[KRN_NN_SCRATCH_BYTES];
+constexpr int KRN_MAX_DEVICES = 64;
+static std::mutex scratch_lock;
+static void* scratch_ptr[KRN_MAX_DEVICES] = {};
+
+// The device address of `scratch` on the calling thread's current device (looked up on that device's first call).
+static void* scratch_on_current_device() {
+  int device = -1;
+  hipError_t rc = hipGetDevice(&device);
+  if (rc != hipSuccess || device < 0 || device >= KRN_MAX_DEVICES) {
+    krn_set_error("gemm_nn_noalloc: no usable current device (%s, ordinal %d)", hipGetErrorString(rc), device);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> hold(scratch_lock);
+  if (scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || ptr == nullptr) {
+      krn_set_error("gemm_nn_noalloc: hipGetSymbolAddress of the scratch array failed: %s", hipGetErrorString(rc));
+      return nullptr;
+    }
+    scratch_ptr[device] = ptr;
+  }
+  return scratch_ptr[device];
+}
+
+extern "C" int64_t krn_gemm_nn_noalloc_limit(void) { return KRN_NN_SCRATCH_BYTES; }
+
+extern "C" int krn_gemm_nn_noalloc(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m,
+                                   int64_t n, int64_t k, int nops, const int* ops, const float* scalars,
+                                   const void* const* vectors, void* stream) {
+  const int64_t need = krn_gemm_nn_workspace(n, k);
+  if (need > KRN_NN_SCRATCH_BYTES) {
+    krn_set_error("gemm_nn_noalloc: B of %lld x %lld needs %lld bytes of scratch; the library holds %lld "
+                  "(use krn_gemm_nn with a workspace)", (long long)k, (long long)n, (long long)need,
+                  (long long)KRN_NN_SCRATCH_BYTES);
+    return -1;
+  }
+  void* bt = nullptr;
+  if (need > 0 && (bt = scratch_on_current_device()) == nullptr) return -1;
+  return gemm_nn_through(in_kind, a, b, c, out_kind, m, n, k, nops, ops, scalars, vectors, bt, stream);
 }
 
 extern "C" int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream) {

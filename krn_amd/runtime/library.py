@@ -47,6 +47,13 @@ def lib() -> ctypes.CDLL:
     ]  # fmt: skip
     handle.krn_gemm_nn_workspace.restype = c_int64
     handle.krn_gemm_nn_workspace.argtypes = [c_int64, c_int64]
+    handle.krn_gemm_nn_noalloc.restype = c_int
+    handle.krn_gemm_nn_noalloc.argtypes = [
+        c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64, c_int, POINTER(c_int),
+        POINTER(c_float), POINTER(c_void_p), c_void_p,
+    ]  # fmt: skip
+    handle.krn_gemm_nn_noalloc_limit.restype = c_int64
+    handle.krn_gemm_nn_noalloc_limit.argtypes = []
     handle.krn_transpose16.restype = c_int
     handle.krn_transpose16.argtypes = [c_void_p, c_void_p, c_int64, c_int64, c_void_p]
     handle.krn_softmax_rows.restype = c_int
@@ -80,6 +87,13 @@ def gemm_nt_call(in_dtype: Dtype, a: int, b: int, c: int, out_dtype: Dtype, m: i
         check(entry(*head, stream), "krn_gemm_nt")
 
     return call
+
+
+def marshal_ops(ops: list[tuple[int, float, int]]):
+    """The (codes, scalars, vectors) arrays of an epilogue chain for the GEMM entry points."""
+    count = len(ops)
+    return ((c_int * max(count, 1))(*(op for op, _, _ in ops)), (c_float * max(count, 1))(*(s for _, s, _ in ops)),
+            (c_void_p * max(count, 1))(*(v for _, _, v in ops)))
 
 
 def gemm_nn_workspace(n: int, k: int) -> int:
