@@ -805,7 +805,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
 // them (32 bytes for fp8): both operands see the same K permutation, so the dot products are unchanged. The ring has
 // STAGES stages per wave, STAGES - 1 slices in flight while one is multiplied. The partial sums meet in LDS, and
 // waves 0..MT-1 each store one 32 x 32 block through the common epilogue.
-template <int FMT, int MT, int WAVES, int STAGES, bool ACT>
+template <int FMT, int MT, int WAVES, int STAGES, bool ACT, int AL = MT * 4>
 __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __restrict__ A,
                                                               const uint8_t* __restrict__ B, void* __restrict__ C,
                                                               int64_t M, int64_t N, int64_t kbytes, int64_t lda,
@@ -816,7 +816,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __re
   constexpr int CH = Unit::kBytes / 32;       // 16-byte registers per lane per MFMA step
   constexpr int STEPS = 4 / CH;               // MFMA steps per 128-byte slice
   constexpr int STAGE = (MT + 1) * 4096;      // one slice: MT * 32 rows of A, then 32 rows of B, 128 bytes each
-  constexpr int LOADS = (MT + 1) * 4;         // DMA instructions per slice
+  constexpr int LOADS = AL + 4;               // DMA instructions per slice: AL of A's rows (8 each), 4 of B's
+  static_assert(AL >= 1 && AL <= MT * 4, "A loads cover at most the ring's A rows");
   constexpr int AHEAD = (STAGES - 1) * LOADS; // loads still in flight when the oldest slice is waited for
   constexpr int RING_WORDS = WAVES * STAGES * STAGE / 4;
   constexpr int RED_WORDS = WAVES * MT * 16 * 64;
@@ -830,13 +831,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __re
   // DMA instruction j fills rows 8 j .. 8 j + 7 of the stage (A's rows first, then B's); lane L lands at position
   // L & 7 of row 8 j + (L >> 3) and so fetches the chunk that the swizzle puts there. Rows past the end of A or B
   // read the last row: their results are never stored.
+  // Only the first AL eight-row groups of A are loaded: the ring rows past them hold whatever the LDS held, and
+  // their results (rows >= 8 AL >= M) are never stored.
   const uint8_t* src[LOADS];
+  int dst[LOADS];
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
-    const int chunk = (lane & 7) ^ (((j & 3) * 4 + (lane >> 4)) & 7);
-    const int64_t row = j * 8 + (lane >> 3);  // row of the stage
-    src[j] = j < MT * 4 ? A + min(row, M - 1) * lda + chunk * 16
-                        : B + min(n0 + row - MT * 32, N - 1) * ldb + chunk * 16;
+    const int g = j < AL ? j : MT * 4 + (j - AL);  // eight-row group of the stage
+    const int chunk = (lane & 7) ^ (((g & 3) * 4 + (lane >> 4)) & 7);
+    const int64_t row = g * 8 + (lane >> 3);  // row of the stage
+    src[j] = j < AL ? A + min(row, M - 1) * lda + chunk * 16 : B + min(n0 + row - MT * 32, N - 1) * ldb + chunk * 16;
+    dst[j] = g * 1024;
   }
   uint8_t* ring = reinterpret_cast<uint8_t*>(lds) + wave * STAGES * STAGE;
   int rd[4];
@@ -856,17 +861,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void gemm_skinny(const uint8_t* __re
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of the stage are done before it is refilled
     const int64_t off = (int64_t)slice * 128;
 #pragma unroll
-    for (int j = 0; j < MT * 4; ++j)
+    for (int j = 0; j < AL; ++j)
       __builtin_amdgcn_global_load_lds((const void*)(src[j] + off),
-                                       (__attribute__((address_space(3))) void*)(ring + stage * STAGE + j * 1024), 16,
+                                       (__attribute__((address_space(3))) void*)(ring + stage * STAGE + dst[j]), 16,
                                        0, 0);
     // B (the weights, read once) streams non-temporally when M <= 32: fp8 M = 1 13.4 -> 11.8 us, M = 16 13.4 ->
     // 12.5 us, W8A8 M = 16 12.6 -> 12.0 us. With four row blocks (M = 128) it was 22 % slower, so A-heavy shapes
     // keep the default policy.
 #pragma unroll
-    for (int j = MT * 4; j < LOADS; ++j)
+    for (int j = AL; j < LOADS; ++j)
       __builtin_amdgcn_global_load_lds((const void*)(src[j] + off),
-                                       (__attribute__((address_space(3))) void*)(ring + stage * STAGE + j * 1024), 16,
+                                       (__attribute__((address_space(3))) void*)(ring + stage * STAGE + dst[j]), 16,
                                        0, MT == 1 ? 2 : 0);
   };
   auto consume = [&](int stage) {
@@ -1001,21 +1006,34 @@ static int launch_pp(const void* a, const void* b, void* c, int64_t m, int64_t n
 template <int FMT, int MT>
 static int launch_skinny_mt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                             int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  // four waves (one per SIMD, all issuing MFMAs: fewer leave bf16 compute-bound at 128 rows) and two stages: the
-  // ring takes 64 KiB for one row block, so two workgroups share a CU and one's reduction and epilogue overlap the
-  // other's stream; 96 to 160 KiB for more rows
-  constexpr int STAGES = 2;
+  // four waves (one per SIMD, all issuing MFMAs: fewer leave bf16 compute-bound at 128 rows). One row block: four
+  // stages (128 KiB; N = 8192 gives one workgroup per CU, and fp8 M = 1 went 11.5 -> 11.2 us against two stages);
+  // more row blocks: two stages, 96 to 160 KiB
+  constexpr int STAGES = MT == 1 ? 4 : 2;
   // an epilogue without activations gets a kernel without their code (a quarter of the size, and no instruction
   // cache misses in the epilogue)
   bool act = false;
   for (int i = 0; i < e.nops; ++i) act |= (e.op[i] & ((1 << VEC_KIND_SHIFT) - 1)) >= RELU;
   const dim3 grid((unsigned)((n + 31) / 32)), block(4 * 64);
-  if (act)
-    hipLaunchKernelGGL((gemm_skinny<FMT, MT, 4, STAGES, true>), grid, block, 0, stream, (const uint8_t*)a,
-                       (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
-  else
-    hipLaunchKernelGGL((gemm_skinny<FMT, MT, 4, STAGES, false>), grid, block, 0, stream, (const uint8_t*)a,
-                       (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  // one row block: only the eight-row groups of A that hold rows < M are loaded
+#define KRN_SKINNY(AL)                                                                                          \
+  do {                                                                                                          \
+    if (act)                                                                                                    \
+      hipLaunchKernelGGL((gemm_skinny<FMT, MT, 4, STAGES, true, AL>), grid, block, 0, stream, (const uint8_t*)a, \
+                         (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);                                 \
+    else                                                                                                        \
+      hipLaunchKernelGGL((gemm_skinny<FMT, MT, 4, STAGES, false, AL>), grid, block, 0, stream, (const uint8_t*)a, \
+                         (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);                                 \
+  } while (0)
+  if constexpr (MT == 1) {
+    if (m <= 8) KRN_SKINNY(1);
+    else if (m <= 16) KRN_SKINNY(2);
+    else if (m <= 24) KRN_SKINNY(3);
+    else KRN_SKINNY(4);
+  } else {
+    KRN_SKINNY(MT * 4);
+  }
+#undef KRN_SKINNY
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     krn_set_error("gemm launch: %s", hipGetErrorString(err));

@@ -119,6 +119,21 @@ def test_int8_skinny_staged_is_bit_exact(device, m, n, k):
     np.testing.assert_array_equal(c.to_host(), a.astype(np.int64) @ w.astype(np.int64).T)
 
 
+# one row block (M <= 32): only the eight-row groups of A holding rows < M are loaded (1 to 4 of them); the ring rows
+# past them hold stale LDS contents whose results are never stored. Every group boundary, with slice counts below,
+# at and above the four-stage ring per wave.
+@pytest.mark.parametrize("m", [1, 7, 8, 9, 16, 17, 24, 25, 32])
+@pytest.mark.parametrize("k", [128, 1024, 128 * 37])
+def test_int8_single_row_block_loads_only_the_rows_it_needs(device, m, k):
+    rng = np.random.default_rng(m * 1000 + k)
+    n = 200
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    c = device.empty(T.i32, m, n)
+    programs.gemm_i8_i32[programs.Tiling(bm=32, bn=32, bk=32)](device.to_device(a), device.to_device(w), c)
+    np.testing.assert_array_equal(c.to_host(), a.astype(np.int64) @ w.astype(np.int64).T)
+
+
 @pytest.mark.parametrize("m,n,k", [(33, 96, 64), (100, 70, 320), (128, 256, 1088)])
 def test_bf16_skinny_staged_agrees_with_the_float64_bound(device, m, n, k):
     rng = np.random.default_rng(6)
