@@ -297,6 +297,64 @@ __device__ __forceinline__ void store_block(const V& block, uint32_t* patch, voi
   patch_store<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
 }
 
+// A whole 32 x 32 float block straight from the MFMA accumulator layout to 16-bit C, without the LDS patch: for the
+// common epilogues (no operation, or float32 scalar multiplies and adds) of a block wholly inside C. Lane L holds
+// column c = L & 31 at rows (r / 4) * 8 + (L / 32) * 4 + r % 4; neighbouring lanes hold columns c and c ^ 1 of the same
+// rows. One DPP swap per register pair (2i, 2i + 1) gives the even lane both columns of row R(2i) and the odd lane
+// both columns of row R(2i + 1), so every lane stores eight 4-byte pairs and each store instruction writes 64-byte
+// row segments. The result is the patch path's bit for bit (same operations, same rounding).
+__device__ __forceinline__ bool direct_epilogue(const Epilogue& e) {
+  if (e.out_kind != BF16 && e.out_kind != F16) return false;
+  for (int i = 0; i < e.nops; ++i)
+    if (e.op[i] != MUL_SCALAR && e.op[i] != ADD_SCALAR) return false;
+  return true;
+}
+
+template <typename V>
+__device__ __forceinline__ void store_block_direct(const V& block, void* C, int64_t ldc, int64_t row0, int64_t col0,
+                                                   const Epilogue& e, int lane) {
+  float v[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) v[r] = block[r];
+  for (int i = 0; i < e.nops; ++i) {
+    const float s = e.scalar[i];
+    if (e.op[i] == MUL_SCALAR) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = __fmul_rn(v[r], s);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = __fadd_rn(v[r], s);
+    }
+  }
+  const int c = lane & 31, half = lane >> 5, odd = c & 1;
+  uint16_t* out = static_cast<uint16_t*>(C);
+  const bool bf = e.out_kind == BF16;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float send = odd ? v[2 * i] : v[2 * i + 1];
+    // quad_perm [1, 0, 3, 2]: exchange with lane ^ 1
+    const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, true));
+    const float lo = odd ? recv : v[2 * i], hi = odd ? v[2 * i + 1] : recv;
+    const int r = 2 * i + odd;
+    const int64_t row = row0 + (r >> 2) * 8 + half * 4 + (r & 3);
+    const uint32_t pair = bf ? ((uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16))
+                             : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
+    __builtin_nontemporal_store(pair, reinterpret_cast<uint32_t*>(out + row * ldc + col0 + (c & ~1)));
+  }
+}
+
+// One accumulator block to C: straight from registers when the block is whole and the epilogue is a common one,
+// else through the LDS patch (all operations, ragged edges, int32 and float32 outputs).
+template <bool INT, typename V>
+__device__ __forceinline__ void store_block_any(const V& block, uint32_t* patch, void* C, int64_t ldc, int64_t row0,
+                                                int64_t col0, int64_t M, int64_t N, const Epilogue& e, int lane,
+                                                bool direct) {
+  if (!INT && direct && row0 + 32 <= M && col0 + 32 <= N)
+    store_block_direct(block, C, ldc, row0, col0, e, lane);
+  else
+    store_block<INT>(block, patch, C, ldc, row0, col0, M, N, e, lane);
+}
+
 // 16 bytes of row `base` starting at byte `kb`, zero past the row's end or for a row outside the matrix. VEC: the
 // row is 16-byte aligned and its length a multiple of 16, so one dwordx4 load does it.
 template <bool VEC>
@@ -640,12 +698,13 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   __syncthreads();  // every wave is done with the ring before its LDS becomes the store patches
 
   uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
+  const bool direct = direct_epilogue(e) && (ldc % 2) == 0 && (uintptr_t)C % 4 == 0;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
-      store_block<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wm * (BM / WM) + i * 32,
-                                 n0 + wn * (BN / WN) + j * 32, M, N, e, lane);
+      store_block_any<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wm * (BM / WM) + i * 32,
+                                     n0 + wn * (BN / WN) + j * 32, M, N, e, lane, direct);
 }
 
 // Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
@@ -787,11 +846,13 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
   __syncthreads();  // every wave is done with the ring before its LDS becomes the store patches
 
   uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
+  const bool direct = direct_epilogue(e) && (ldc % 2) == 0 && (uintptr_t)C % 4 == 0;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
-      store_block<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wr + i * 32, n0 + wc + j * 32, M, N, e, lane);
+      store_block_any<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wr + i * 32, n0 + wc + j * 32, M, N, e, lane,
+                                     direct);
 }
 
 // Skinny products (M <= 128), the HBM-bound shapes: B (N x K) is streamed from HBM once and A (M x K) is read by
@@ -1003,13 +1064,9 @@ static int launch_pp(const void* a, const void* b, void* c, int64_t m, int64_t n
   return 0;
 }
 
-template <int FMT, int MT>
+template <int FMT, int MT, int STAGES>
 static int launch_skinny_mt(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                             int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  // four waves (one per SIMD, all issuing MFMAs: fewer leave bf16 compute-bound at 128 rows). One row block: four
-  // stages (128 KiB; N = 8192 gives one workgroup per CU, and fp8 M = 1 went 11.5 -> 11.2 us against two stages);
-  // more row blocks: two stages, 96 to 160 KiB
-  constexpr int STAGES = MT == 1 ? 4 : 2;
   // an epilogue without activations gets a kernel without their code (a quarter of the size, and no instruction
   // cache misses in the epilogue)
   bool act = false;
@@ -1042,15 +1099,22 @@ static int launch_skinny_mt(const void* a, const void* b, void* c, int64_t m, in
   return 0;
 }
 
-// M <= 128 rows with 16-byte aligned rows of a multiple of 128 bytes: one workgroup per 32 output columns.
+// M <= 128 rows with 16-byte aligned rows of a multiple of 128 bytes: one workgroup per 32 output columns, four
+// waves (one per SIMD, all issuing MFMAs: fewer leave bf16 compute-bound at 128 rows). One row block and at most one
+// workgroup per CU (N <= 8192): a four-stage ring per wave (128 KiB; fp8 M = 1 11.5 -> 11.2 us against two stages);
+// more workgroups than CUs: two stages (64 KiB), so that two workgroups share a CU and one's reduction and epilogue
+// overlap the other's stream (W8A8 M = 16, N = 14336: 15.4 us, against 18.7 us with four stages); more row blocks:
+// two stages, 96 to 160 KiB.
 template <int FMT>
 static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                          int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
   switch ((m + 31) / 32) {
-    case 1: return launch_skinny_mt<FMT, 1>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
-    case 2: return launch_skinny_mt<FMT, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
-    case 3: return launch_skinny_mt<FMT, 3>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
-    case 4: return launch_skinny_mt<FMT, 4>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    case 1:
+      return (n + 31) / 32 <= 256 ? launch_skinny_mt<FMT, 1, 4>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream)
+                                  : launch_skinny_mt<FMT, 1, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    case 2: return launch_skinny_mt<FMT, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    case 3: return launch_skinny_mt<FMT, 3, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    case 4: return launch_skinny_mt<FMT, 4, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   }
   krn_set_error("gemm: %lld rows are too many for the skinny kernel", (long long)m);
   return -1;
