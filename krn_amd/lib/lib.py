@@ -73,17 +73,18 @@ class NoCandidate(LookupError):
 
 class Candidate(ABC):
     """One implementation of one operation. `unavailable` is why it cannot run on this machine at all, `refusal` why
-    it does not take this problem; `run` only enqueues, on the given stream, and never synchronizes."""
+    it does not take this problem; `run` only enqueues, on the given stream, and never synchronizes. The `target`
+    arguments mirror the reference's signatures (lib.py:201-235); this build serves gfx950 only and ignores them."""
 
     name: str
     op: Op
     origin: Origin
 
-    def unavailable(self) -> str | None:
+    def unavailable(self, target=None) -> str | None:
         return None
 
     @abstractmethod
-    def refusal(self, problem: Problem) -> str | None: ...
+    def refusal(self, problem: Problem, target=None) -> str | None: ...
 
     @abstractmethod
     def run(self, problem: Problem, operands: Operands, stream: Stream) -> None: ...
@@ -94,10 +95,10 @@ class Host(Candidate):
 
     name, op, origin = "host", Op.MATMUL, Origin.OURS
 
-    def unavailable(self) -> str | None:
+    def unavailable(self, target=None) -> str | None:
         return "krn_amd has no host path: every product runs on the GPU"
 
-    def refusal(self, problem: Problem) -> str | None:
+    def refusal(self, problem: Problem, target=None) -> str | None:
         return self.unavailable()
 
     def run(self, problem: Problem, operands: Operands, stream: Stream) -> None:

@@ -216,14 +216,14 @@ _session = Session()
 class HipblasLt(Candidate):
     name, op, origin = "hipblaslt", Op.MATMUL, Origin.VENDOR
 
-    def unavailable(self) -> str | None:
+    def unavailable(self, target=None) -> str | None:
         try:
             api()
         except LibraryNotFound as error:
             return str(error)
         return None
 
-    def refusal(self, problem: Problem) -> str | None:
+    def refusal(self, problem: Problem, target=None) -> str | None:
         return refusal(problem)
 
     def run(self, problem: Problem, operands: Operands, stream: Stream) -> None:

@@ -25,7 +25,7 @@ TILE = {"bm": 64, "bn": 64, "bk": 32}
 class Ours(Candidate):
     name, op, origin = "ours", Op.MATMUL, Origin.OURS
 
-    def refusal(self, problem: Problem) -> str | None:
+    def refusal(self, problem: Problem, target=None) -> str | None:
         if len(set(problem.dtypes)) != 1 or problem.dtypes[0] not in (F16, BF16, F32):
             names = ", ".join(str(d) for d in problem.dtypes)
             return f"matmul_epilogue takes one F for a, b, bias and out, f16, bf16 or f32; got {names}"
