@@ -544,6 +544,12 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   constexpr int LOADS = LOADS_A + LOADS_B;   // load instructions per wave per slice
   constexpr int STAGE_BYTES = (BM + BN) * BKB;
   constexpr int VMCNT = (STAGES - 2) * LOADS;
+  // With three or more stages the A loads of a slice go between the first MFMAs and the B loads between the MFMAs
+  // after the barrier, one load every four MFMAs: the workgroup's 32 loads of a slice no longer arrive at the
+  // texture unit as one burst (bf16 8192^3 +2.5 %). At the barrier of slice kt the loads younger than slice kt + 1
+  // are then slices kt + 2 .. kt + STAGES - 2 and the A loads of slice kt + STAGES - 1.
+  constexpr bool SPREAD = STAGES >= 3;
+  constexpr int VMCNT_SPLIT = SPREAD ? (STAGES - 3) * LOADS + LOADS_A : VMCNT;
   static_assert(KS % 2 == 0, "an even number of MFMA steps per slice");
   static_assert(LOADS_A * ROWS_PER_LOAD * (THREADS / 64) == BM && LOADS_B * ROWS_PER_LOAD * (THREADS / 64) == BN,
                 "the tile splits into whole wave loads");
@@ -608,6 +614,39 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   } while (0)
   // vmcnt(n) with lgkmcnt and expcnt left alone (gfx9 s_waitcnt encoding), then every LDS read of this wave done
   // and the workgroup barrier
+#define KRN_ISSUE_A(slice)                                                                                      \
+  do {                                                                                                          \
+    uint8_t* stage = lds + ((slice) % STAGES) * STAGE_BYTES;                                                    \
+    const int koff = (slice) * BKB;                                                                             \
+    _Pragma("unroll") for (int j = 0; j < LOADS_A; ++j)                                                         \
+        buffer_to_lds16(a_rsrc, stage + (wave * LOADS_A + j) * 1024, a_off_g[j], koff);                         \
+  } while (0)
+#define KRN_ISSUE_B(slice)                                                                                      \
+  do {                                                                                                          \
+    uint8_t* stage = lds + ((slice) % STAGES) * STAGE_BYTES;                                                    \
+    const int koff = (slice) * BKB;                                                                             \
+    _Pragma("unroll") for (int j = 0; j < LOADS_B; ++j)                                                         \
+        buffer_to_lds16(b_rsrc, stage + BM * BKB + (wave * LOADS_B + j) * 1024, b_off_g[j], koff);              \
+  } while (0)
+  // scheduling of the spread form: per load, MFMA read MFMA read MFMA load MFMA read (one load every four MFMAs)
+#define KRN_SPREAD_A()                                                                                         \
+  do {                                                                                                          \
+    _Pragma("unroll") for (int q = 0; q < LOADS_A; ++q) {                                                       \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     \
+    }                                                                                                           \
+  } while (0)
+#define KRN_SPREAD_B()                                                                                         \
+  do {                                                                                                          \
+    _Pragma("unroll") for (int q = 0; q < LOADS_B; ++q) {                                                       \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     \
+    }                                                                                                           \
+  } while (0)
 #define KRN_PUBLISH(n)                                                                                          \
   do {                                                                                                          \
     __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | ((n) & 15) | (((n) >> 4) << 14));                              \
@@ -658,18 +697,29 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
 #pragma unroll
     for (int k = 0; k < KS; k += 2) {
       KRN_FRAGS(f1, kt, k + 1);
-      if (k == 0) KRN_ISSUE(kt + STAGES - 1);
-      KRN_MMA(f0);
-      KRN_WITH_READS();
-      if (k == 0) KRN_WITH_LOADS();
+      if constexpr (SPREAD) {
+        if (k == 0) KRN_ISSUE_A(kt + STAGES - 1);
+        KRN_MMA(f0);
+        KRN_SPREAD_A();
+      } else {
+        if (k == 0) KRN_ISSUE(kt + STAGES - 1);
+        KRN_MMA(f0);
+        KRN_WITH_READS();
+        if (k == 0) KRN_WITH_LOADS();
+      }
       if (k + 2 < KS) {
         KRN_FRAGS(f0, kt, k + 2);
       } else {
-        KRN_PUBLISH(VMCNT);
+        KRN_PUBLISH(VMCNT_SPLIT);
         KRN_FRAGS(f0, kt + 1, 0);
+        if constexpr (SPREAD) KRN_ISSUE_B(kt + STAGES - 1);
       }
       KRN_MMA(f1);
-      KRN_WITH_READS();
+      if constexpr (SPREAD) {
+        KRN_SPREAD_B();
+      } else {
+        KRN_WITH_READS();
+      }
     }
   }
   // drain: the last STAGES - 1 slices are already in flight
@@ -695,6 +745,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
 #undef KRN_MMA
 #undef KRN_WITH_READS
 #undef KRN_WITH_LOADS
+#undef KRN_ISSUE_A
+#undef KRN_ISSUE_B
+#undef KRN_SPREAD_A
+#undef KRN_SPREAD_B
   __syncthreads();  // every wave is done with the ring before its LDS becomes the store patches
 
   uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
