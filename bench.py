@@ -170,6 +170,18 @@ def gemm_w8a8(device, steps, warmup, rng, m, n=14336, k=4096):
     return ms, 2.0 * m * n * k, n * k + m * k + 4 * (m + n) + 2 * m * n
 
 
+def cpu_model() -> str:
+    """The host CPU's model name, as /proc/cpuinfo gives it."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(a_words: np.ndarray, b_words: np.ndarray, budget_s: float = 12.0, threads: int = 1) -> dict:
     """The oracle C backend (krn's CPU lowering: one thread per block, fmaf in k order) running the same gemm_nt
     program with 128 x 128 tiles over whole output tiles of the 8192^3 problem until `budget_s`: on one core (the
@@ -200,6 +212,7 @@ def cpu_baseline(a_words: np.ndarray, b_words: np.ndarray, budget_s: float = 12.
         "value": flops / elapsed / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "cpu": cpu_model(),
         "kind": "port",
         "sample": f"{blocks} of {(n // tile) ** 2} 128x128 output tiles of the 8192^3 bf16 gemm_nt program "
                   f"(full K), oracle C backend, {threads} thread{'s' if threads > 1 else ''}, {elapsed:.1f} s",

@@ -1408,12 +1408,54 @@ extern "C" int krn_gemm_nn_noalloc(int in_kind, const void* a, const void* b, vo
   return gemm_nn_through(in_kind, a, b, c, out_kind, m, n, k, nops, ops, scalars, vectors, bt, stream);
 }
 
+// Whole 128 x 128 tiles (rows and cols multiples of 128, 16-byte aligned): rows land in LDS with 16-byte loads (256
+// contiguous bytes per 16 lanes); each thread then reads one 8 x 8 block with eight 16-byte LDS reads, transposes it
+// in registers (v_perm_b32 pairs the 16-bit halves of two rows) and writes eight 16-byte pieces of output rows, 256
+// contiguous bytes per 16 lanes (8192^2: 70 -> 56 us).
+__global__ __launch_bounds__(256) void transpose16_tiles(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
+                                                         int64_t rows, int64_t cols) {
+  constexpr int P = 128 + 8;  // LDS row pitch in elements: 16 bytes of padding keep the block reads off one bank
+  __shared__ __attribute__((aligned(16))) uint16_t tile[128 * P];
+  const int t = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.y * 128, c0 = (int64_t)blockIdx.x * 128;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int row = p * 16 + (t >> 4), cb = (t & 15) * 8;
+    *reinterpret_cast<u32x4*>(tile + row * P + cb) =
+        __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(in + (r0 + row) * cols + c0 + cb));
+  }
+  __syncthreads();
+  const int bi = t & 15, bj = t >> 4;
+  u32x4 r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = *reinterpret_cast<const u32x4*>(tile + (bi * 8 + i) * P + bj * 8);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;  // the high or the low halves of two words
+    u32x4 o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = __builtin_amdgcn_perm(r[2 * w + 1][j >> 1], r[2 * w][j >> 1], sel);
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(out + (c0 + bj * 8 + j) * rows + r0 + bi * 8));
+  }
+}
+
 extern "C" int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream) {
   if (rows < 0 || cols < 0) {
     krn_set_error("transpose: negative extent");
     return -1;
   }
   if (rows == 0 || cols == 0) return 0;
+  if (rows % 128 == 0 && cols % 128 == 0 && (uintptr_t)in % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+      cols / 128 <= 0x7fffffff && rows / 128 <= 65535) {
+    hipLaunchKernelGGL(transpose16_tiles, dim3((unsigned)(cols / 128), (unsigned)(rows / 128)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint16_t*)in, (uint16_t*)out, rows, cols);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+      krn_set_error("transpose launch: %s", hipGetErrorString(err));
+      return (int)err;
+    }
+    return 0;
+  }
   const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
   if (gx > 0x7fffffff || gy > 65535) {
     krn_set_error("transpose: %lld x %lld exceeds the grid limit", (long long)rows, (long long)cols);

@@ -56,3 +56,14 @@ def test_gemm_nn_refuses_a_small_workspace_and_other_kinds(device):
     assert call(3, a.pointer, b.pointer, c.pointer, library.kind(BF16), m, n, k, 0, None, None, None,
                 workspace.pointer, n * k * 2, None) != 0  # fp8 operands: not an NN product
     assert b"bf16 or f16" in library.lib().krn_amd_last_error()
+
+
+@pytest.mark.parametrize("rows,cols", [(8192, 1024), (256, 384), (128, 128), (100, 130), (129, 256), (1, 7), (300, 1)])
+def test_transpose16_is_exact_on_whole_tiles_and_ragged_edges(device, rows, cols):
+    """krn_transpose16 (the NN operand's transpose): whole 128 x 128 tiles take the register-transposing kernel, other
+    extents the LDS-tile one; both bit-exact."""
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = rng.integers(0, 1 << 16, (rows, cols), dtype=np.uint16)
+    src, dst = device.to_device(x, T.bf16), device.empty(T.bf16, cols, rows)
+    library.transpose16(src.pointer, dst.pointer, rows, cols, device.default_stream.handle)
+    np.testing.assert_array_equal(dst.to_host(), x.T)
