@@ -297,45 +297,88 @@ __device__ __forceinline__ void store_block(const V& block, uint32_t* patch, voi
   patch_store<INT>(patch, C, ldc, row0, col0, M, N, e, lane);
 }
 
-// A whole 32 x 32 float block straight from the MFMA accumulator layout to 16-bit C, without the LDS patch: for the
-// common epilogues (no operation, or float32 scalar multiplies and adds) of a block wholly inside C. Lane L holds
-// column c = L & 31 at rows (r / 4) * 8 + (L / 32) * 4 + r % 4; neighbouring lanes hold columns c and c ^ 1 of the same
-// rows. One DPP swap per register pair (2i, 2i + 1) gives the even lane both columns of row R(2i) and the odd lane
-// both columns of row R(2i + 1), so every lane stores eight 4-byte pairs and each store instruction writes 64-byte
-// row segments. The result is the patch path's bit for bit (same operations, same rounding).
+// The direct epilogue: whole 32 x 32 blocks straight from the MFMA accumulator layout to 16-bit C, without the LDS
+// patch, for epilogues of at most two operations that are float32 scalars or row/column vectors (no activation):
+// the headline bf16 product, the fp8 product's `acc * (scale_a * scale_b)`, the W8A8 dequantisation
+// `acc * scale_a[m] * scale_w[n]`. Lane L holds column c = L & 31 at rows R(r) = (r / 4) * 8 + (L / 32) * 4 + r % 4;
+// neighbouring lanes hold columns c and c ^ 1 of the same rows. One DPP swap per register pair (2i, 2i + 1) gives the
+// even lane both columns of row R(2i) and the odd lane both columns of row R(2i + 1), so every lane stores eight
+// 4-byte pairs and each store instruction writes 64-byte row segments. The operations and their rounding are the
+// patch path's, so the result is the same bit for bit.
+constexpr int DIRECT_OPS = 2;
+
 __device__ __forceinline__ bool direct_epilogue(const Epilogue& e) {
   if (e.out_kind != BF16 && e.out_kind != F16) return false;
+  if (e.nops > DIRECT_OPS) return false;
   for (int i = 0; i < e.nops; ++i)
-    if (e.op[i] != MUL_SCALAR && e.op[i] != ADD_SCALAR) return false;
+    if ((e.op[i] & ((1 << VEC_KIND_SHIFT) - 1)) >= RELU) return false;
   return true;
 }
 
-template <typename V>
-__device__ __forceinline__ void store_block_direct(const V& block, void* C, int64_t ldc, int64_t row0, int64_t col0,
+// The vector operands of a wave's TM x TN blocks, fetched for all blocks at once before any is stored: for a per-row
+// operation the 16 rows R(r) of each row block, for a per-column one the lane's column of each column block.
+template <int TM, int TN>
+struct DirectVectors {
+  float row[DIRECT_OPS][TM][16];
+  float col[DIRECT_OPS][TN];
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void direct_vectors(DirectVectors<TM, TN>& dv, const Epilogue& e, int64_t row0,
+                                               int64_t col0, int lane) {
+  const int c = lane & 31, half = lane >> 5;
+#pragma unroll
+  for (int q = 0; q < DIRECT_OPS; ++q) {
+    if (q >= e.nops) break;
+    const int op = e.op[q] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[q] >> VEC_KIND_SHIFT;
+    if (op % 3 == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          dv.row[q][i][r] = bits_value(kind, vec_bits(e.vec[q], kind, row0 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3)));
+    } else if (op % 3 == 2) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) dv.col[q][j] = bits_value(kind, vec_bits(e.vec[q], kind, col0 + j * 32 + c));
+    }
+  }
+}
+
+template <bool INT, int TM, int TN, typename V>
+__device__ __forceinline__ void store_block_direct(const V& block, const DirectVectors<TM, TN>& dv, int i, int j,
+                                                   void* C, int64_t ldc, int64_t row0, int64_t col0,
                                                    const Epilogue& e, int lane) {
   float v[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) v[r] = block[r];
-  for (int i = 0; i < e.nops; ++i) {
-    const float s = e.scalar[i];
-    if (e.op[i] == MUL_SCALAR) {
+  for (int r = 0; r < 16; ++r) v[r] = INT ? (float)(int32_t)block[r] : (float)block[r];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) v[r] = __fmul_rn(v[r], s);
+  for (int q = 0; q < DIRECT_OPS; ++q) {
+    if (q >= e.nops) break;
+    const int op = e.op[q] & ((1 << VEC_KIND_SHIFT) - 1);
+    const bool mul = op < 3;
+    if (op % 3 == 0) {
+      const float s = e.scalar[q];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = mul ? __fmul_rn(v[r], s) : __fadd_rn(v[r], s);
+    } else if (op % 3 == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) v[r] = mul ? __fmul_rn(v[r], dv.row[q][i][r]) : __fadd_rn(v[r], dv.row[q][i][r]);
     } else {
+      const float s = dv.col[q][j];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) v[r] = __fadd_rn(v[r], s);
+      for (int r = 0; r < 16; ++r) v[r] = mul ? __fmul_rn(v[r], s) : __fadd_rn(v[r], s);
     }
   }
   const int c = lane & 31, half = lane >> 5, odd = c & 1;
   uint16_t* out = static_cast<uint16_t*>(C);
   const bool bf = e.out_kind == BF16;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float send = odd ? v[2 * i] : v[2 * i + 1];
+  for (int k = 0; k < 8; ++k) {
+    const float send = odd ? v[2 * k] : v[2 * k + 1];
     // quad_perm [1, 0, 3, 2]: exchange with lane ^ 1
     const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, true));
-    const float lo = odd ? recv : v[2 * i], hi = odd ? v[2 * i + 1] : recv;
-    const int r = 2 * i + odd;
+    const float lo = odd ? recv : v[2 * k], hi = odd ? v[2 * k + 1] : recv;
+    const int r = 2 * k + odd;
     const int64_t row = row0 + (r >> 2) * 8 + half * 4 + (r & 3);
     const uint32_t pair = bf ? ((uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16))
                              : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
@@ -343,16 +386,30 @@ __device__ __forceinline__ void store_block_direct(const V& block, void* C, int6
   }
 }
 
-// One accumulator block to C: straight from registers when the block is whole and the epilogue is a common one,
-// else through the LDS patch (all operations, ragged edges, int32 and float32 outputs).
-template <bool INT, typename V>
-__device__ __forceinline__ void store_block_any(const V& block, uint32_t* patch, void* C, int64_t ldc, int64_t row0,
-                                                int64_t col0, int64_t M, int64_t N, const Epilogue& e, int lane,
-                                                bool direct) {
-  if (!INT && direct && row0 + 32 <= M && col0 + 32 <= N)
-    store_block_direct(block, C, ldc, row0, col0, e, lane);
-  else
-    store_block<INT>(block, patch, C, ldc, row0, col0, M, N, e, lane);
+// A wave's TM x TN accumulator blocks to C. When the wave's whole region lies inside C and the epilogue is one the
+// direct path takes, every block goes straight from registers; otherwise each block goes through the LDS patch (all
+// operations, ragged edges, int32 and float32 outputs).
+template <bool INT, int TM, int TN, typename Acc>
+__device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* patch, void* C, int64_t ldc,
+                                           int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
+                                           int lane) {
+  const bool direct = direct_epilogue(e) && (ldc % 2) == 0 && (uintptr_t)C % 4 == 0 && row0 + 32 * TM <= M &&
+                      col0 + 32 * TN <= N;
+  if (direct) {
+    DirectVectors<TM, TN> dv;
+    direct_vectors(dv, e, row0, col0, lane);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        store_block_direct<INT>(acc[i][j], dv, i, j, C, ldc, row0 + i * 32, col0 + j * 32, e, lane);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      store_block<INT>(acc[i][j], patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, e, lane);
 }
 
 // 16 bytes of row `base` starting at byte `kb`, zero past the row's end or for a row outside the matrix. VEC: the
@@ -752,13 +809,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   __syncthreads();  // every wave is done with the ring before its LDS becomes the store patches
 
   uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
-  const bool direct = direct_epilogue(e) && (ldc % 2) == 0 && (uintptr_t)C % 4 == 0;
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-      store_block_any<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wm * (BM / WM) + i * 32,
-                                     n0 + wn * (BN / WN) + j * 32, M, N, e, lane, direct);
+  store_tile<FMT == FMT_I8>(acc, patch, C, ldc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), M, N, e, lane);
 }
 
 // Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
@@ -900,13 +951,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pp(const uint8_t* __restrict__ A,
   __syncthreads();  // every wave is done with the ring before its LDS becomes the store patches
 
   uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
-  const bool direct = direct_epilogue(e) && (ldc % 2) == 0 && (uintptr_t)C % 4 == 0;
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-      store_block_any<FMT == FMT_I8>(acc[i][j], patch, C, ldc, m0 + wr + i * 32, n0 + wc + j * 32, M, N, e, lane,
-                                     direct);
+  store_tile<FMT == FMT_I8>(acc, patch, C, ldc, m0 + wr, n0 + wc, M, N, e, lane);
 }
 
 // Skinny products (M <= 128), the HBM-bound shapes: B (N x K) is streamed from HBM once and A (M x K) is read by
