@@ -331,16 +331,18 @@ __device__ __forceinline__ void direct_vectors(DirectVectors<TM, TN>& dv, const 
   for (int q = 0; q < DIRECT_OPS; ++q) {
     if (q >= e.nops) break;
     const int op = e.op[q] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[q] >> VEC_KIND_SHIFT;
-    if (op % 3 == 1) {
+    // every element is assigned on every path, so the arrays stay in registers
+    const bool per_row = op % 3 == 1, per_col = op % 3 == 2;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dv.row[q][i][r] = bits_value(kind, vec_bits(e.vec[q], kind, row0 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3)));
-    } else if (op % 3 == 2) {
+      for (int r = 0; r < 16; ++r)
+        dv.row[q][i][r] =
+            per_row ? bits_value(kind, vec_bits(e.vec[q], kind, row0 + i * 32 + (r >> 2) * 8 + half * 4 + (r & 3)))
+                    : 0.0f;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) dv.col[q][j] = bits_value(kind, vec_bits(e.vec[q], kind, col0 + j * 32 + c));
-    }
+    for (int j = 0; j < TN; ++j)
+      dv.col[q][j] = per_col ? bits_value(kind, vec_bits(e.vec[q], kind, col0 + j * 32 + c)) : 0.0f;
   }
 }
 
@@ -405,11 +407,15 @@ __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* p
         store_block_direct<INT>(acc[i][j], dv, i, j, C, ldc, row0 + i * 32, col0 + j * 32, e, lane);
     return;
   }
+  // The out-of-line store takes the epilogue by address. Passing the kernel argument itself would copy it to private
+  // memory at kernel entry, in every wave, whichever path the wave takes (80 bytes a lane, 42 MB per bf16 8192^3
+  // launch); this copy is made only on this path.
+  const Epilogue local = e;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
-      store_block<INT>(acc[i][j], patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, e, lane);
+      store_block<INT>(acc[i][j], patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, local, lane);
 }
 
 // 16 bytes of row `base` starting at byte `kb`, zero past the row's end or for a row outside the matrix. VEC: the
