@@ -43,8 +43,18 @@ def test_plan_kinds(name, kind):
 
 def test_attention_program_lowers_to_the_attention_kernel():
     consts = {"t": {"bq": 64, "bk": 64, "d": 128, "causal": True}}
-    plan = cdna4.lower(capture(KERNELS, "flash_attention_bf16", consts=consts))
+    kernel = capture(KERNELS, "flash_attention_bf16", consts=consts)
+    plan = cdna4.lower(kernel)
     assert isinstance(plan, cdna4.AttentionPlan) and plan.d == 128 and plan.causal
+    assert not any("flash-attention" in reason for reason in cdna4.why_generic(kernel))
+
+
+def test_attention_the_kernel_does_not_serve_lowers_generically_and_says_why():
+    """Head dimension 32 is outside the attention kernel: the program runs on the generic lowering, and the reason
+    names the flash-attention match, so `explain()` reports the slower route instead of taking it silently."""
+    kernel = capture(KERNELS, "flash_attention_bf16", consts={"t": {"bq": 64, "bk": 64, "d": 32, "causal": True}})
+    assert isinstance(cdna4.lower(kernel), cdna4.GenericPlan)
+    assert any("flash-attention" in reason for reason in cdna4.why_generic(kernel))
 
 
 
