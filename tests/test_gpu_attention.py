@@ -70,3 +70,67 @@ def test_f16_flash_attention_matches_the_oracle_emulator(device, causal):
     want = np.zeros((heads, seq, d), np.float16)
     emulate.run(capture(KERNELS, "flash_attention", consts={"t": consts}), launch, [q, k, v, want, scale])
     np.testing.assert_allclose(o.to_host().astype(np.float32), want.astype(np.float32), atol=2e-3)
+
+
+def program_attention(q, k, v, scale, causal):
+    """The flash-attention program's result in float64: p = exp2(scale * q.k - max) (the scale carries log2 e), the
+    causal mask keeps key positions <= query positions, o = p v / sum p (tile_programs.flash_attention_bf16)."""
+    q, k, v = (x.astype(np.float64) for x in (q, k, v))
+    s = (q @ k.transpose(0, 2, 1)) * scale
+    if causal:
+        sq, sk = s.shape[-2:]
+        s = np.where(np.arange(sk)[None, :] <= np.arange(sq)[:, None], s, -np.inf)
+    p = np.exp2(s - s.max(axis=-1, keepdims=True))
+    return (p / p.sum(axis=-1, keepdims=True)) @ v
+
+
+def run_bf16_attention(device, words, causal, scale, d):
+    heads, sq = words[0].shape[:2]
+    o = device.empty(T.bf16, heads, sq, d)
+    tiling = programs.Attention(bq=64, bk=64, d=d, causal=causal)
+    programs.flash_attention_bf16(tiling, *(device.to_device(w, T.bf16) for w in words), o, scale,
+                                  launch=Blocks(-(-sq // 64), heads))
+    return bf16_values(o.to_host()).astype(np.float64)
+
+
+@pytest.mark.parametrize("sq,sk,causal", [(200, 520, False), (200, 520, True), (300, 70, True), (300, 70, False),
+                                          (64, 1, False), (1, 300, True), (1, 300, False)])
+def test_bf16_flash_attention_with_different_query_and_key_lengths(device, sq, sk, causal):
+    """Queries and keys of different lengths: the program runs over k's own length, and the causal mask compares
+    absolute positions, so a query row at or past the last key sees every key."""
+    heads, d = 2, 128
+    rng = np.random.default_rng(sq * 1000 + sk)
+    words = [bf16_words(rng.standard_normal((heads, n, d)).astype(np.float32)) for n in (sq, sk, sk)]
+    scale = math.log2(math.e) / math.sqrt(d)
+    got = run_bf16_attention(device, words, causal, scale, d)
+    np.testing.assert_allclose(got, program_attention(*(bf16_values(w) for w in words), scale, causal), atol=2e-2)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_flash_attention_when_the_running_maximum_keeps_rising(device, causal):
+    """Scores that climb by about 9 (in log2 units) every 64 keys: the kernel refreshes its exponent base only when
+    a row maximum beats it by more than 8, so here it rescales the output and the row sum on nearly every tile, and
+    the earlier tiles still weigh about 2^-9 each: a missed or doubled rescale shows at once."""
+    heads, seq, d = 2, 512, 128
+    rng = np.random.default_rng(9)
+    q = np.ones((heads, seq, d), np.float32)
+    level = 0.55 * (np.arange(seq) // 64)
+    k = level[None, :, None] + 0.05 * rng.standard_normal((heads, seq, d))
+    v = rng.standard_normal((heads, seq, d))
+    words = [bf16_words(x.astype(np.float32)) for x in (q, k, v)]
+    scale = math.log2(math.e) / math.sqrt(d)
+    want = program_attention(*(bf16_values(w) for w in words), scale, causal)
+    np.testing.assert_allclose(run_bf16_attention(device, words, causal, scale, d), want, atol=2e-2)
+
+
+@pytest.mark.parametrize("factor", [-1.0, 0.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bf16_flash_attention_with_a_scale_that_is_not_positive(device, factor, causal):
+    """A negative scale reverses the order of the scores, so the row maximum cannot be taken on the raw scores; a
+    zero scale makes every valid key weigh the same. The kernel scales every score first on that path."""
+    heads, seq, d = 2, 200, 64
+    rng = np.random.default_rng(11)
+    words = [bf16_words(rng.standard_normal((heads, seq, d)).astype(np.float32)) for _ in range(3)]
+    scale = factor * math.log2(math.e) / math.sqrt(d)
+    want = program_attention(*(bf16_values(w) for w in words), scale, causal)
+    np.testing.assert_allclose(run_bf16_attention(device, words, causal, scale, d), want, atol=2e-2)
