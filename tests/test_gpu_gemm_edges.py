@@ -1,0 +1,103 @@
+"""Edges of the tile GEMM on gfx950: empty outputs, special values and the full int8 range.
+
+The reference's products are IEEE arithmetic (its CPU backend is one `fmaf` per k, reference
+src/krn/compiler/emit.py:791-796), so a NaN operand makes its whole output row or column NaN, an infinity makes it
+infinite, and infinity times zero is NaN. Each shape below is chosen to reach one of the kernel families (the
+mid-size and whole-tile pipelines, the skinny kernel and the bounds-checked tiles), because each has its own
+epilogue store."""
+
+import numpy as np
+import pytest
+
+from krn_amd import T
+from oracle.numerics import bf16_values, bf16_words, e4m3_decode, e4m3_encode
+from tests.helpers import agree_bound
+from tests.kernels import tile_programs as programs
+
+pytestmark = pytest.mark.gpu
+
+TILING = programs.Tiling(bm=64, bn=64, bk=32)
+
+
+@pytest.mark.parametrize("m,n,k", [(0, 64, 128), (64, 0, 128), (0, 0, 0)])
+def test_an_empty_output_launches_nothing_and_raises_nothing(device, m, n, k):
+    a = device.to_device(np.zeros((m, k), np.uint16), T.bf16)
+    b = device.to_device(np.zeros((n, k), np.uint16), T.bf16)
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_nt[TILING](a, b, c)
+    device.default_stream.sync()
+    assert c.to_host().shape == (m, n)
+
+
+def classes(x: np.ndarray) -> np.ndarray:
+    """0 finite, 1 NaN, 2 +inf, 3 -inf."""
+    return np.select([np.isnan(x), x == np.inf, x == -np.inf], [1, 2, 3], 0)
+
+
+# (m, n, k): mid-size pipeline, whole 256 x 256 pipeline, skinny, bounds-checked tiles (K not whole 128-byte slices)
+SPECIAL_SHAPES = [(512, 512, 256), (2048, 4096, 128), (16, 640, 512), (300, 200, 136)]
+
+
+@pytest.mark.parametrize("m,n,k", SPECIAL_SHAPES)
+def test_bf16_special_values_propagate_as_in_ieee_arithmetic(device, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k)).astype(np.float32)
+    a[3, 5] = np.nan          # row 3: NaN
+    a[7, 9] = np.inf          # row 7: +-inf, and NaN in the columns whose B row is 0 at k = 9
+    b[11, 9] = 0.0
+    b[13, 2] = -np.inf        # column 13: +-inf, NaN where A's row meets it with 0 or with the +inf above
+    a[8, 2] = 0.0
+    aw, bw = bf16_words(a), bf16_words(b)
+    av, bv = bf16_values(aw).astype(np.float64), bf16_values(bw).astype(np.float64)
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_nt[TILING](device.to_device(aw, T.bf16), device.to_device(bw, T.bf16), c)
+    got = bf16_values(c.to_host()).astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        want = np.einsum("ik,jk->ij", av, bv)
+    np.testing.assert_array_equal(classes(got), classes(want))
+    assert np.isnan(got[3]).all() and np.isnan(got[8, 13]) and np.isnan(got[7, 11])
+    # a finite entry's A row and B row hold no special value, so it is the product of the operands with the
+    # special values zeroed: krn's float32 bound plus one bf16 rounding there
+    finite = classes(want) == 0
+    clean_a, clean_b = np.where(np.isfinite(av), av, 0.0), np.where(np.isfinite(bv), bv, 0.0)
+    reference, bound = agree_bound(clean_a, clean_b.T, k)
+    bound = bound + np.abs(reference) * 2.0**-8 + 2.0**-133
+    assert np.all(np.abs(got - reference)[finite] <= bound[finite])
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 512, 256), (16, 640, 512), (100, 200, 200)])
+def test_fp8_nan_codes_make_their_row_and_column_nan(device, m, n, k):
+    """e4m3fn has no infinity; 0x7F and 0xFF are NaN (reference narrow.py:94-110). A NaN code in A poisons its row,
+    one in B its column, through the scale epilogue as well."""
+    rng = np.random.default_rng(7)
+    a = e4m3_encode(rng.standard_normal((m, k)).astype(np.float32))
+    b = e4m3_encode(rng.standard_normal((n, k)).astype(np.float32))
+    a[2, 17], b[5, 40] = 0x7F, 0xFF
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_fp8[TILING](device.to_device(a, T.f8e4m3fn), device.to_device(b, T.f8e4m3fn), c, 0.5, 0.25)
+    got = bf16_values(c.to_host()).astype(np.float64)
+    want_nan = np.zeros((m, n), bool)
+    want_nan[2, :] = True
+    want_nan[:, 5] = True
+    np.testing.assert_array_equal(np.isnan(got), want_nan)
+    da, db = e4m3_decode(a).astype(np.float64), e4m3_decode(b).astype(np.float64)
+    da[2], db[5] = 0.0, 0.0
+    keep = ~want_nan
+    scale = 0.5 * 0.25
+    reference = (da @ db.T) * scale
+    bound = (8 * 2.0**-24 * (k + 8) * (np.abs(da) @ np.abs(db).T)) * scale + np.abs(reference) * 2.0**-8 * 1.01
+    assert np.all(np.abs(got - reference)[keep] <= bound[keep] + 1e-30)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 768, 384), (16, 640, 512), (257, 129, 96)])
+def test_int8_gemm_over_the_full_int8_range_is_bit_exact(device, m, n, k):
+    """-128 included (the reference's generators stop at -127): the int32 result is exact."""
+    rng = np.random.default_rng(m * n + k)
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    a[0, :] = -128
+    b[0, :] = -128
+    c = device.empty(T.i32, m, n)
+    programs.gemm_i8_i32[TILING](device.to_device(a), device.to_device(b), c)
+    np.testing.assert_array_equal(c.to_host(), a.astype(np.int64) @ b.astype(np.int64).T)
