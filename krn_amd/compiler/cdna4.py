@@ -25,7 +25,7 @@ import dataclasses
 from dataclasses import dataclass, field
 
 from krn_amd.compiler import ir
-from krn_amd.dtypes import BF16, F8E4M3, F16, F32, I8, I32, PY_INT, Dtype
+from krn_amd.dtypes import BF16, F8E4M3, F16, F32, I8, I32, Dtype
 
 GEMM_OPERANDS = (BF16, F16, F8E4M3, I8)
 ACTIVATIONS = {ir.Fn.RELU: "relu", ir.Fn.GELU: "gelu", ir.Fn.SILU: "silu"}

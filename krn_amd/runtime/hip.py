@@ -28,7 +28,7 @@ from krn_amd import dtypes as D
 from krn_amd.compiler import cdna4, hipgen, space
 from krn_amd.compiler import ir
 from krn_amd.compiler.capture import TargetError, capture
-from krn_amd.dtypes import BF16, F32, Dtype
+from krn_amd.dtypes import Dtype
 from krn_amd.frontend import Blocks, Kernel, Tensor, const_fields
 from krn_amd.runtime import api, hipapi, library, roctx
 from krn_amd.runtime.api import Backend, Bound, Device, Event, Graph, Launcher, Stream, current_stream

@@ -21,7 +21,7 @@ import numpy as np
 
 from krn_amd.compiler import ir
 from krn_amd.compiler.space import geometry, runtime_args
-from krn_amd.dtypes import BF16, BOOL, F8E4M3, F16, I8, I32, NUMPY, PY_FLOAT, PY_INT, Dtype
+from krn_amd.dtypes import BF16, BOOL, F16, I32, NUMPY, PY_FLOAT, PY_INT, Dtype
 from krn_amd.frontend import Blocks
 from oracle.numerics import bf16_round, e4m3_decode, e4m3_encode, fma32
 

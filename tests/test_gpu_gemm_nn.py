@@ -3,7 +3,6 @@ B stored K x N), through the C ABI: it transposes B into the caller's workspace 
 result is bit-identical to krn_gemm_nt on B transposed on the host; a workspace that is too small is refused before
 anything is enqueued."""
 
-import ctypes
 
 import numpy as np
 import pytest
