@@ -45,8 +45,7 @@ struct Half;
 template <>
 struct Half<true> {
   __device__ static uint32_t pack(float lo, float hi) {
-    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-    return __builtin_bit_cast(uint32_t, bf2{(__bf16)lo, (__bf16)hi});  // v_cvt_pk_bf16_f32, nearest even
+    return f2bf2(lo, hi);  // v_cvt_pk_bf16_f32, nearest even
   }
   __device__ static uint16_t from(float x) { return f2bf(x); }
   __device__ static void mma(f32x16& c, u32x4 a, u32x4 b) {

@@ -268,7 +268,7 @@ __device__ __forceinline__ void patch_store_inline(uint32_t* patch, void* C, int
   uint32_t h[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c)
-    h[c] = e.out_kind == BF16 ? ((uint32_t)f2bf(v[2 * c]) | ((uint32_t)f2bf(v[2 * c + 1]) << 16))
+    h[c] = e.out_kind == BF16 ? f2bf2(v[2 * c], v[2 * c + 1])
                               : ((uint32_t)f2h(v[2 * c]) | ((uint32_t)f2h(v[2 * c + 1]) << 16));
   uint16_t* out = static_cast<uint16_t*>(C) + m * ldc + n;
   if (whole) {
@@ -348,8 +348,7 @@ __device__ __forceinline__ void direct_vectors(DirectVectors<TM, TN>& dv, const 
 
 template <bool INT, int TM, int TN, typename V>
 __device__ __forceinline__ void store_block_direct(const V& block, const DirectVectors<TM, TN>& dv, int i, int j,
-                                                   void* C, int64_t ldc, int64_t row0, int64_t col0,
-                                                   const Epilogue& e, int lane) {
+                                                   uint16_t* lane_out, int64_t ldc, const Epilogue& e, int lane) {
   float v[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) v[r] = INT ? (float)(int32_t)block[r] : (float)block[r];
@@ -371,8 +370,7 @@ __device__ __forceinline__ void store_block_direct(const V& block, const DirectV
       for (int r = 0; r < 16; ++r) v[r] = mul ? __fmul_rn(v[r], s) : __fadd_rn(v[r], s);
     }
   }
-  const int c = lane & 31, half = lane >> 5, odd = c & 1;
-  uint16_t* out = static_cast<uint16_t*>(C);
+  const int odd = lane & 1;
   const bool bf = e.out_kind == BF16;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -380,11 +378,11 @@ __device__ __forceinline__ void store_block_direct(const V& block, const DirectV
     // quad_perm [1, 0, 3, 2]: exchange with lane ^ 1
     const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, true));
     const float lo = odd ? recv : v[2 * k], hi = odd ? v[2 * k + 1] : recv;
-    const int r = 2 * k + odd;
-    const int64_t row = row0 + (r >> 2) * 8 + half * 4 + (r & 3);
-    const uint32_t pair = bf ? ((uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16))
-                             : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
-    __builtin_nontemporal_store(pair, reinterpret_cast<uint32_t*>(out + row * ldc + col0 + (c & ~1)));
+    const uint32_t pair = bf ? f2bf2(lo, hi) : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
+    // accumulator register 2k + odd holds row ((2k + odd) >> 2) * 8 + half * 4 + ((2k + odd) & 3); the lane's part
+    // (half * 4 + odd) is in lane_out, the rest is the same for the whole wave
+    const int64_t step = (int64_t)((k >> 1) * 8 + (k & 1) * 2) + (int64_t)(i * 32);
+    __builtin_nontemporal_store(pair, reinterpret_cast<uint32_t*>(lane_out + step * ldc + j * 32));
   }
 }
 
@@ -400,11 +398,13 @@ __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* p
   if (direct) {
     DirectVectors<TM, TN> dv;
     direct_vectors(dv, e, row0, col0, lane);
+    // each lane stores a column pair at (c & ~1) of rows half * 4 + odd + wave-uniform steps
+    const int c = lane & 31;
+    uint16_t* lane_out = static_cast<uint16_t*>(C) + (row0 + (lane >> 5) * 4 + (c & 1)) * ldc + col0 + (c & ~1);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        store_block_direct<INT>(acc[i][j], dv, i, j, C, ldc, row0 + i * 32, col0 + j * 32, e, lane);
+      for (int j = 0; j < TN; ++j) store_block_direct<INT>(acc[i][j], dv, i, j, lane_out, ldc, e, lane);
     return;
   }
   // The out-of-line store takes the epilogue by address. Passing the kernel argument itself would copy it to private
