@@ -3,8 +3,8 @@
 // This is the lowering of krn's tile contraction `acc += a[rows, ks] @ b[cols, ks].transpose()` followed by
 // `c[rows, cols] = f(acc).to(dtype)` (reference compiler/ir.py:309-315 Accumulate, compiler/emit.py:788-821). One
 // workgroup owns a BM x BN output tile, four waves split it 2 x 2, and every wave keeps its accumulators in
-// registers as 32x32 MFMA blocks. Main loops: `gemm_pipe` (bf16/f16/int8) and `gemm_pp` (fp8) for whole 256 x 256
-// tiles (rings of direct-to-LDS slices, see there; the same loop on 128 x 128 tiles for up to one wave of them),
+// registers as 32x32 MFMA blocks. Main loops: `gemm_quad` (bf16/f16), `gemm_pipe` (int8) and `gemm_pp` (fp8) for
+// whole 256 x 256 tiles (see each; `gemm_pipe` also on 128 x 128 tiles for up to one wave of them),
 // `gemm_skinny` for M <= 128 (rings of direct-to-LDS slices per wave), and `gemm_tile` for the rest (128-byte
 // slices staged through registers, bounds-checked, double buffered). All end in the same epilogue, `patch_put` + `patch_store`.
 //
@@ -818,6 +818,149 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   store_tile<FMT == FMT_I8>(acc, patch, C, ldc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), M, N, e, lane);
 }
 
+// Four-wave main loop for whole 256 x 256 bf16/f16 tiles with K a multiple of 128 bytes. Each wave owns a 128 x 128
+// quarter (wave w: rows 128 (w >> 1), columns 128 (w & 1)), 16 accumulator blocks in AGPRs, one wave per SIMD.
+// 128-byte K slices go global -> registers -> LDS: slice kt + 2 is loaded into registers while slice kt multiplies,
+// and slice kt + 1 is written from those registers into the other of two LDS stages; the same 16 loads and 16 writes
+// per wave and slice as hipBLASLt's kernel makes. Every instruction of a slice has a fixed place (sched_barrier): per
+// MFMA step 16 MFMAs, each followed by at most one LDS read of the next step's fragments, one LDS write and one
+// global load, so the matrix core is never left waiting behind a burst of memory instructions; the one barrier per
+// slice comes after the eighth MFMA of the last step, once this wave's writes of slice kt + 1 have landed, and the
+// first fragments of slice kt + 1 are read in the shadow of the last eight MFMAs. Past the end the loads re-read the
+// last slice and the writes go to the stage that is not read again, so every slice runs the same code.
+// bf16 8192^3: 3-5 % faster than the eight-wave ring with direct-to-LDS slices, whose loads cost about a sixth of its
+// loop in LDS bandwidth (eight waves of 64 x 128 read 96 KiB of fragments per 64-byte slice, four of 128 x 128 read
+// 64 KiB per 128-byte slice).
+template <int FMT>
+__global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                                                    void* __restrict__ C, int64_t M, int64_t N, int64_t kbytes,
+                                                    int64_t lda, int64_t ldb, int64_t ldc, Epilogue e) {
+  typedef Mfma<FMT> Unit;
+  typedef typename Unit::Acc Acc;
+  static_assert(Unit::kBytes == 32, "one 16-byte chunk per lane and operand per MFMA");
+  constexpr int BM = 256, BN = 256, BKB = 128;
+  constexpr int STAGE = (BM + BN) * BKB;  // 64 KiB: A rows, then B rows, 128 bytes each, chunks swizzled by swz8
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
+  int tm, tn;
+  tile_of((int)((M + BM - 1) / BM), (int)((N + BN - 1) / BN), tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, r32 = lane & 31;
+  // The buffer resources must be visibly wave-uniform, or every load is wrapped in a readfirstlane loop.
+  auto uniform = [](const void* p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const void*)(((uint64_t)hi << 32) | lo);
+  };
+  const int64_t a_bytes = __builtin_amdgcn_readfirstlane((int)min((M - m0) * lda, (int64_t)0x7fffffff));
+  const int64_t b_bytes = __builtin_amdgcn_readfirstlane((int)min((N - n0) * ldb, (int64_t)0x7fffffff));
+  const __amdgpu_buffer_rsrc_t a_rsrc = panel_rsrc(uniform(A + m0 * lda), a_bytes),
+                              b_rsrc = panel_rsrc(uniform(B + n0 * ldb), b_bytes);
+  // wave w stages rows 64 w .. 64 w + 63 of A and of B, 8 rows (1 KiB) per load; lane i takes row i / 8 and the
+  // global chunk that belongs at slot i % 8
+  const int lrow = lane >> 3, lslot = lane & 7;
+  uint32_t ga[8], gb[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = wave * 64 + j * 8 + lrow;
+    ga[j] = (uint32_t)(row * lda + ((lslot ^ swz8(row)) * 16));
+    gb[j] = (uint32_t)(row * ldb + ((lslot ^ swz8(row)) * 16));
+  }
+  // fragment of MFMA step s: chunk 2 s + half of row r32 of a 32-row block (the swizzle depends on r32 only)
+  const int sw = (r32 >> 1) & 7;
+  int rd[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) rd[s] = r32 * 128 + (((2 * s + half) ^ sw) * 16);
+  const int wr = wave * 8192 + lane * 16;
+  const int nk = (int)(kbytes / BKB);  // >= 2 (host)
+
+  u32x4 stg[16];       // one slice of this wave's rows: 0-7 A, 8-15 B
+  u32x4 F0[8], F1[8];  // fragments of two MFMA steps: 0-3 the A blocks, 4-7 the B blocks
+  Acc acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = Acc{};
+
+#define KQ_LOAD(q, slice)                                                                                      \
+  do {                                                                                                         \
+    if ((q) < 8)                                                                                               \
+      stg[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ga[(q) & 7], (slice) * BKB, 0)); \
+    else                                                                                                       \
+      stg[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, gb[(q) & 7], (slice) * BKB, 0)); \
+  } while (0)
+#define KQ_WRITE(q, slice)                                                                                     \
+  *reinterpret_cast<u32x4*>(lds + ((slice) & 1) * STAGE + ((q) < 8 ? 0 : BM * BKB) + wr + ((q) & 7) * 1024) = stg[q]
+#define KQ_READ(F, r, slice, s)                                                                                \
+  F[r] = *reinterpret_cast<const u32x4*>(                                                                      \
+      lds + ((slice) & 1) * STAGE + rd[s] +                                                                    \
+      ((r) < 4 ? (wm * 128 + (r) * 32) * 128 : BM * BKB + (wn * 128 + ((r) - 4) * 32) * 128))
+#define KQ_FENCE() __builtin_amdgcn_sched_barrier(0)
+#define KQ_MMA(F, m) Unit::step(acc[(m) >> 2][(m) & 3], &F[(m) >> 2], &F[4 + ((m) & 3)])
+  // fragments in the order the next step's MFMAs use them: A0 B0 B1 B2 B3 A1 A2 A3
+#define KQ_ORDER(x) ((x) == 0 ? 0 : (x) <= 4 ? 4 + (x) - 1 : (x) - 4)
+  // steps 0-2: after MFMA m, the next step's fragment m / 2 (m even); item 4 s + m / 4 of this wave's share of
+  // slice kt + 1 written (m % 4 == 1) and then reloaded with slice `ls` (m % 4 == 3)
+#define KQ_STEP(CUR, NXT, s, kt, ls)                                                                           \
+  do {                                                                                                         \
+    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
+      KQ_MMA(CUR, m);                                                                                          \
+      KQ_FENCE();                                                                                              \
+      if (m % 2 == 0) { KQ_READ(NXT, KQ_ORDER(m / 2), kt, (s) + 1); KQ_FENCE(); }                             \
+      if (m % 4 == 1) { KQ_WRITE((s) * 4 + m / 4, (kt) + 1); KQ_FENCE(); }                                    \
+      if (m % 4 == 3) { KQ_LOAD((s) * 4 + m / 4, ls); KQ_FENCE(); }                                           \
+    }                                                                                                          \
+  } while (0)
+  // step 3: items 12-15 written and reloaded under the first eight MFMAs, then the barrier (this wave's LDS
+  // traffic done), then the first fragments of slice kt + 1 under the last eight
+#define KQ_STEP3(CUR, NXT, kt, ls)                                                                             \
+  do {                                                                                                         \
+    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
+      KQ_MMA(CUR, m);                                                                                          \
+      KQ_FENCE();                                                                                              \
+      if (m < 8 && m % 2 == 0) { KQ_WRITE(12 + m / 2, (kt) + 1); KQ_FENCE(); }                                 \
+      if (m < 8 && m % 2 == 1) { KQ_LOAD(12 + m / 2, ls); KQ_FENCE(); }                                        \
+      if (m == 7) {                                                                                            \
+        __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0), vmcnt and expcnt left alone */                     \
+        __builtin_amdgcn_s_barrier();                                                                          \
+        KQ_FENCE();                                                                                            \
+      }                                                                                                        \
+      if (m >= 7 && m < 15) { KQ_READ(NXT, KQ_ORDER(m - 7), (kt) + 1, 0); KQ_FENCE(); }                       \
+    }                                                                                                          \
+  } while (0)
+
+#pragma unroll
+  for (int q = 0; q < 16; ++q) KQ_LOAD(q, 0);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) KQ_WRITE(q, 0);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) KQ_LOAD(q, 1);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int x = 0; x < 8; ++x) KQ_READ(F0, x, 0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int ls = min(kt + 2, nk - 1);
+    KQ_STEP(F0, F1, 0, kt, ls);
+    KQ_STEP(F1, F0, 1, kt, ls);
+    KQ_STEP(F0, F1, 2, kt, ls);
+    KQ_STEP3(F1, F0, kt, ls);
+  }
+#undef KQ_LOAD
+#undef KQ_WRITE
+#undef KQ_READ
+#undef KQ_FENCE
+#undef KQ_MMA
+#undef KQ_ORDER
+#undef KQ_STEP
+#undef KQ_STEP3
+  __syncthreads();  // every wave is done with the stages before its LDS becomes the store patches
+  uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
+  store_tile<false>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
+}
+
 // Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
 // 32x32x32 steps, fp8: one 32x32x64 step per slice -- 512 MFMA cycles per wave in every format). Eight waves form two
 // groups of four: group g owns rows [128 g, 128 g + 128) of the tile, and within a group wave q owns the 64 x 128
@@ -1151,6 +1294,24 @@ static int launch_pipe(const void* a, const void* b, void* c, int64_t m, int64_t
   return 0;
 }
 
+template <int FMT>
+static int launch_quad(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                       int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+  const int64_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
+  if (tiles > 0x7fffffff) {
+    krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
+    return -1;
+  }
+  hipLaunchKernelGGL((gemm_quad<FMT>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
+                     (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    krn_set_error("gemm launch: %s", hipGetErrorString(err));
+    return (int)err;
+  }
+  return 0;
+}
+
 template <int FMT, int STAGES>
 static int launch_pp(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                      int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
@@ -1225,21 +1386,24 @@ static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64
   return -1;
 }
 
-// 256 x 256 tiles (ragged at the edges): for bf16/f16 a ring of four 64-byte K slices (two MFMA steps each); for fp8
-// the ping-pong ring of four 64-byte slices (one MFMA step each); for int8 two 128-byte slices (four MFMA steps
-// each).
+// 256 x 256 tiles (ragged at the edges): for bf16/f16 the four-wave loop over register-staged 128-byte slices (K of
+// at least two slices; otherwise a ring of four 64-byte slices); for fp8 the ping-pong ring of four 64-byte slices
+// (one MFMA step each); for int8 two 128-byte slices of the eight-wave ring (the four-wave loop is 19 % slower on
+// W8A8 4096 x 14336 x 4096).
 template <int FMT>
 static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
   // fp8: the ping-pong loop (one 64x64 f8f6f4 MFMA step per 64-byte slice keeps its memory phase short enough to
-  // hide behind the other group's MFMAs). bf16/f16 and int8: eight waves (4 x 2, each 64 x 128 of the tile) that
-  // interleave their own LDS reads with their MFMAs.
-  if constexpr (FMT == FMT_FP8)
+  // hide behind the other group's MFMAs). int8: eight waves (4 x 2, each 64 x 128 of the tile) that interleave their
+  // own LDS reads with their MFMAs. bf16/f16: four waves of 128 x 128 in a fixed instruction order.
+  if constexpr (FMT == FMT_FP8) {
     return launch_pp<FMT, 4>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
-  else if constexpr (FMT == FMT_I8)
+  } else if constexpr (FMT == FMT_I8) {
     return launch_pipe<FMT, 256, 256, 4, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
-  else
+  } else {
+    if (kbytes % 128 == 0 && kbytes >= 256) return launch_quad<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
     return launch_pipe<FMT, 256, 256, 4, 2, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  }
 }
 
 // Up to one wave of 128 x 128 tiles (at most 256 tiles): the pipelined loop on 128 x 128 tiles with four waves, a
