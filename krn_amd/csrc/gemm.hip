@@ -3,7 +3,7 @@
 // This is the lowering of krn's tile contraction `acc += a[rows, ks] @ b[cols, ks].transpose()` followed by
 // `c[rows, cols] = f(acc).to(dtype)` (reference compiler/ir.py:309-315 Accumulate, compiler/emit.py:788-821). One
 // workgroup owns a BM x BN output tile, four waves split it 2 x 2, and every wave keeps its accumulators in
-// registers as 32x32 MFMA blocks. Main loops: `gemm_quad` (bf16/f16), `gemm_pipe` (int8) and `gemm_pp` (fp8) for
+// registers as 32x32 MFMA blocks. Main loops: `gemm_quad` (bf16/f16/fp8), `gemm_pipe` (int8) and `gemm_pp` (fp8 with one slice) for
 // whole 256 x 256 tiles (see each; `gemm_pipe` also on 128 x 128 tiles for up to one wave of them),
 // `gemm_skinny` for M <= 128 (rings of direct-to-LDS slices per wave), and `gemm_tile` for the rest (128-byte
 // slices staged through registers, bounds-checked, double buffered). All end in the same epilogue, `patch_put` + `patch_store`.
@@ -389,7 +389,19 @@ __device__ __forceinline__ void store_block_direct(const V& block, const DirectV
 // A wave's TM x TN accumulator blocks to C. When the wave's whole region lies inside C and the epilogue is one the
 // direct path takes, every block goes straight from registers; otherwise each block goes through the LDS patch (all
 // operations, ragged edges, int32 and float32 outputs).
-template <bool INT, int TM, int TN, typename Acc>
+//
+// AGPR: the accumulators live in AGPRs (the four-wave loop's 256 of them). Each block is then copied to VGPRs right
+// before it is stored, by ordered reads; left to itself the compiler copies all of them at the end of the loop and
+// spills most of them to private memory.
+template <typename V>
+__device__ __forceinline__ V agpr_block(const V& x) {
+  V y;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(y[r]) : "a"(x[r]) : "memory");
+  return y;
+}
+
+template <bool INT, int TM, int TN, typename Acc, bool AGPR = false>
 __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* patch, void* C, int64_t ldc,
                                            int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
                                            int lane) {
@@ -404,7 +416,12 @@ __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* p
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) store_block_direct<INT>(acc[i][j], dv, i, j, lane_out, ldc, e, lane);
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (AGPR)
+          store_block_direct<INT>(agpr_block(acc[i][j]), dv, i, j, lane_out, ldc, e, lane);
+        else
+          store_block_direct<INT>(acc[i][j], dv, i, j, lane_out, ldc, e, lane);
+      }
     return;
   }
   // The out-of-line store takes the epilogue by address. Passing the kernel argument itself would copy it to private
@@ -415,7 +432,10 @@ __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* p
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
-      store_block<INT>(acc[i][j], patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, local, lane);
+      if constexpr (AGPR)
+        store_block<INT>(agpr_block(acc[i][j]), patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, local, lane);
+      else
+        store_block<INT>(acc[i][j], patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, local, lane);
 }
 
 // 16 bytes of row `base` starting at byte `kb`, zero past the row's end or for a row outside the matrix. VEC: the
@@ -818,7 +838,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   store_tile<FMT == FMT_I8>(acc, patch, C, ldc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), M, N, e, lane);
 }
 
-// Four-wave main loop for whole 256 x 256 bf16/f16 tiles with K a multiple of 128 bytes. Each wave owns a 128 x 128
+// Four-wave main loop for whole 256 x 256 bf16/f16/fp8 tiles with K a multiple of 128 bytes. Each wave owns a 128 x 128
 // quarter (wave w: rows 128 (w >> 1), columns 128 (w & 1)), 16 accumulator blocks in AGPRs, one wave per SIMD.
 // 128-byte K slices go global -> registers -> LDS: slice kt + 2 is loaded into registers while slice kt multiplies,
 // and slice kt + 1 is written from those registers into the other of two LDS stages; the same 16 loads and 16 writes
@@ -837,8 +857,10 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
                                                     int64_t lda, int64_t ldb, int64_t ldc, Epilogue e) {
   typedef Mfma<FMT> Unit;
   typedef typename Unit::Acc Acc;
-  static_assert(Unit::kBytes == 32, "one 16-byte chunk per lane and operand per MFMA");
   constexpr int BM = 256, BN = 256, BKB = 128;
+  constexpr int CH = Unit::kBytes / 32;  // 16-byte chunks per lane and operand of one MFMA (bf16/f16/int8 1, fp8 2)
+  constexpr int NS = BKB / Unit::kBytes; // MFMA steps per slice (4 or 2)
+  static_assert(CH == 1 || CH == 2, "32 or 64 bytes of K per MFMA");
   constexpr int STAGE = (BM + BN) * BKB;  // 64 KiB: A rows, then B rows, 128 bytes each, chunks swizzled by swz8
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
   int tm, tn;
@@ -868,16 +890,18 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
     ga[j] = (uint32_t)(row * lda + ((lslot ^ swz8(row)) * 16));
     gb[j] = (uint32_t)(row * ldb + ((lslot ^ swz8(row)) * 16));
   }
-  // fragment of MFMA step s: chunk 2 s + half of row r32 of a 32-row block (the swizzle depends on r32 only)
+  // fragment of MFMA step s: chunks (2 s + half) CH + c of row r32 of a 32-row block (the swizzle depends on r32 only)
   const int sw = (r32 >> 1) & 7;
-  int rd[4];
+  int rd[NS][CH];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) rd[s] = r32 * 128 + (((2 * s + half) ^ sw) * 16);
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) rd[s][c] = r32 * 128 + ((((2 * s + half) * CH + c) ^ sw) * 16);
   const int wr = wave * 8192 + lane * 16;
   const int nk = (int)(kbytes / BKB);  // >= 2 (host)
 
   u32x4 stg[16];       // one slice of this wave's rows: 0-7 A, 8-15 B
-  u32x4 F0[8], F1[8];  // fragments of two MFMA steps: 0-3 the A blocks, 4-7 the B blocks
+  u32x4 F0[8 * CH], F1[8 * CH];  // fragments of two MFMA steps: 0-3 the A blocks, 4-7 the B blocks, CH chunks each
   Acc acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -893,12 +917,13 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
   } while (0)
 #define KQ_WRITE(q, slice)                                                                                     \
   *reinterpret_cast<u32x4*>(lds + ((slice) & 1) * STAGE + ((q) < 8 ? 0 : BM * BKB) + wr + ((q) & 7) * 1024) = stg[q]
-#define KQ_READ(F, r, slice, s)                                                                                \
-  F[r] = *reinterpret_cast<const u32x4*>(                                                                      \
-      lds + ((slice) & 1) * STAGE + rd[s] +                                                                    \
+#define KQ_READC(F, r, c, slice, s)                                                                            \
+  F[(r) * CH + (c)] = *reinterpret_cast<const u32x4*>(                                                         \
+      lds + ((slice) & 1) * STAGE + rd[s][c] +                                                                 \
       ((r) < 4 ? (wm * 128 + (r) * 32) * 128 : BM * BKB + (wn * 128 + ((r) - 4) * 32) * 128))
 #define KQ_FENCE() __builtin_amdgcn_sched_barrier(0)
-#define KQ_MMA(F, m) Unit::step(acc[(m) >> 2][(m) & 3], &F[(m) >> 2], &F[4 + ((m) & 3)])
+#define KQ_READ(F, r, slice, s) KQ_READC(F, r, 0, slice, s)
+#define KQ_MMA(F, m) Unit::step(acc[(m) >> 2][(m) & 3], &F[((m) >> 2) * CH], &F[(4 + ((m) & 3)) * CH])
   // fragments in the order the next step's MFMAs use them: A0 B0 B1 B2 B3 A1 A2 A3
 #define KQ_ORDER(x) ((x) == 0 ? 0 : (x) <= 4 ? 4 + (x) - 1 : (x) - 4)
   // steps 0-2: after MFMA m, the next step's fragment m / 2 (m even); item 4 s + m / 4 of this wave's share of
@@ -930,6 +955,42 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
       if (m >= 7 && m < 15) { KQ_READ(NXT, KQ_ORDER(m - 7), (kt) + 1, 0); KQ_FENCE(); }                       \
     }                                                                                                          \
   } while (0)
+  // fp8 (two steps of 64-cycle MFMAs per slice). Step 0: after MFMA m the next step's fragment chunk m (of
+  // KQ_ORDER(m / 2)), then item m / 2 of slice kt + 1 written (m even) or reloaded with slice `ls` (m odd).
+#define KQ8_STEP0(CUR, NXT, kt, ls)                                                                            \
+  do {                                                                                                         \
+    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
+      KQ_MMA(CUR, m);                                                                                          \
+      KQ_FENCE();                                                                                              \
+      KQ_READC(NXT, KQ_ORDER(m / 2), m % 2, kt, 1);                                                            \
+      KQ_FENCE();                                                                                              \
+      if (m % 2 == 0) KQ_WRITE(m / 2, (kt) + 1); else KQ_LOAD(m / 2, ls);                                      \
+      KQ_FENCE();                                                                                              \
+    }                                                                                                          \
+  } while (0)
+  // step 1: items 8-15 written under the first seven MFMAs, the barrier after the eighth, then the first step's
+  // fragments of slice kt + 1 (two chunks per MFMA) and the reloads of items 8-15
+#define KQ8_STEP1(CUR, NXT, kt, ls)                                                                            \
+  do {                                                                                                         \
+    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
+      KQ_MMA(CUR, m);                                                                                          \
+      KQ_FENCE();                                                                                              \
+      if (m < 7) { KQ_WRITE(8 + m, (kt) + 1); KQ_FENCE(); }                                                    \
+      if (m == 6) { KQ_WRITE(15, (kt) + 1); KQ_FENCE(); }                                                      \
+      if (m == 7) {                                                                                            \
+        __builtin_amdgcn_s_waitcnt(0xc07f);                                                                    \
+        __builtin_amdgcn_s_barrier();                                                                          \
+        KQ_FENCE();                                                                                            \
+      }                                                                                                        \
+      if (m >= 7 && m < 15) {                                                                                  \
+        KQ_READC(NXT, KQ_ORDER(m - 7), 0, (kt) + 1, 0);                                                        \
+        KQ_READC(NXT, KQ_ORDER(m - 7), 1, (kt) + 1, 0);                                                        \
+        KQ_FENCE();                                                                                            \
+        KQ_LOAD(8 + m - 7, ls);                                                                                \
+        KQ_FENCE();                                                                                            \
+      }                                                                                                        \
+    }                                                                                                          \
+  } while (0)
 
 #pragma unroll
   for (int q = 0; q < 16; ++q) KQ_LOAD(q, 0);
@@ -939,18 +1000,34 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
   for (int q = 0; q < 16; ++q) KQ_LOAD(q, 1);
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_s_barrier();
+  // in the order the loop's last step reads them, so that the first MFMAs wait on a partial LDS count in every
+  // iteration (a reordered prologue forces a full wait at the top of the loop)
+  KQ_FENCE();
 #pragma unroll
-  for (int x = 0; x < 8; ++x) KQ_READ(F0, x, 0, 0);
+  for (int x = 0; x < 8; ++x)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      KQ_READC(F0, KQ_ORDER(x), c, 0, 0);
+      KQ_FENCE();
+    }
   for (int kt = 0; kt < nk; ++kt) {
     const int ls = min(kt + 2, nk - 1);
-    KQ_STEP(F0, F1, 0, kt, ls);
-    KQ_STEP(F1, F0, 1, kt, ls);
-    KQ_STEP(F0, F1, 2, kt, ls);
-    KQ_STEP3(F1, F0, kt, ls);
+    if constexpr (NS == 4) {
+      KQ_STEP(F0, F1, 0, kt, ls);
+      KQ_STEP(F1, F0, 1, kt, ls);
+      KQ_STEP(F0, F1, 2, kt, ls);
+      KQ_STEP3(F1, F0, kt, ls);
+    } else {
+      KQ8_STEP0(F0, F1, kt, ls);
+      KQ8_STEP1(F1, F0, kt, ls);
+    }
   }
 #undef KQ_LOAD
 #undef KQ_WRITE
 #undef KQ_READ
+#undef KQ_READC
+#undef KQ8_STEP0
+#undef KQ8_STEP1
 #undef KQ_FENCE
 #undef KQ_MMA
 #undef KQ_ORDER
@@ -958,7 +1035,7 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
 #undef KQ_STEP3
   __syncthreads();  // every wave is done with the stages before its LDS becomes the store patches
   uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
-  store_tile<false>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
+  store_tile<FMT == FMT_I8, 4, 4, Acc, true>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
 }
 
 // Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
@@ -1393,10 +1470,12 @@ static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64
 template <int FMT>
 static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  // fp8: the ping-pong loop (one 64x64 f8f6f4 MFMA step per 64-byte slice keeps its memory phase short enough to
-  // hide behind the other group's MFMAs). int8: eight waves (4 x 2, each 64 x 128 of the tile) that interleave their
-  // own LDS reads with their MFMAs. bf16/f16: four waves of 128 x 128 in a fixed instruction order.
+  // bf16/f16 and fp8: four waves of 128 x 128 in a fixed instruction order (fp8 8192^3 7 % faster than the
+  // eight-wave ping-pong, which keeps the one-slice K = 128 case). int8: eight waves (4 x 2, each 64 x 128 of the
+  // tile) that interleave their own LDS reads with their MFMAs (the four-wave loop measured 10 % slower on W8A8
+  // M = 4096, whose K of 32 slices leaves more of the time to the prologue and epilogue).
   if constexpr (FMT == FMT_FP8) {
+    if (kbytes >= 256) return launch_quad<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
     return launch_pp<FMT, 4>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   } else if constexpr (FMT == FMT_I8) {
     return launch_pipe<FMT, 256, 256, 4, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
