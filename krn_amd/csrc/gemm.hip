@@ -900,7 +900,11 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
   const int wr = wave * 8192 + lane * 16;
   const int nk = (int)(kbytes / BKB);  // >= 2 (host)
 
-  u32x4 stg[16];       // one slice of this wave's rows: 0-7 A, 8-15 B
+  // register sets of one slice of this wave's rows each (0-7 A, 8-15 B): with two, a slice is loaded two slices
+  // before it is written to LDS, which covers an L2 miss under load (about 3000 cycles against 2048 per slice);
+  // fp8's fragments take the registers of a second set
+  constexpr int NSET = CH == 1 ? 2 : 1;
+  u32x4 stg[NSET][16];
   u32x4 F0[8 * CH], F1[8 * CH];  // fragments of two MFMA steps: 0-3 the A blocks, 4-7 the B blocks, CH chunks each
   Acc acc[4][4];
 #pragma unroll
@@ -911,12 +915,12 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
 #define KQ_LOAD(q, slice)                                                                                      \
   do {                                                                                                         \
     if ((q) < 8)                                                                                               \
-      stg[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ga[(q) & 7], (slice) * BKB, 0)); \
+      stg[SET_][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ga[(q) & 7], (slice) * BKB, 0)); \
     else                                                                                                       \
-      stg[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, gb[(q) & 7], (slice) * BKB, 0)); \
+      stg[SET_][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, gb[(q) & 7], (slice) * BKB, 0)); \
   } while (0)
 #define KQ_WRITE(q, slice)                                                                                     \
-  *reinterpret_cast<u32x4*>(lds + ((slice) & 1) * STAGE + ((q) < 8 ? 0 : BM * BKB) + wr + ((q) & 7) * 1024) = stg[q]
+  *reinterpret_cast<u32x4*>(lds + ((slice) & 1) * STAGE + ((q) < 8 ? 0 : BM * BKB) + wr + ((q) & 7) * 1024) = stg[SET_][q]
 #define KQ_READC(F, r, c, slice, s)                                                                            \
   F[(r) * CH + (c)] = *reinterpret_cast<const u32x4*>(                                                         \
       lds + ((slice) & 1) * STAGE + rd[s][c] +                                                                 \
@@ -992,12 +996,24 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
     }                                                                                                          \
   } while (0)
 
+  {
+    // slice 0 through set 0 into stage 0; slices 1 .. NSET into the sets (set of slice j: j % NSET)
+    constexpr int SET_ = 0;
 #pragma unroll
-  for (int q = 0; q < 16; ++q) KQ_LOAD(q, 0);
+    for (int q = 0; q < 16; ++q) KQ_LOAD(q, 0);
 #pragma unroll
-  for (int q = 0; q < 16; ++q) KQ_WRITE(q, 0);
+    for (int q = 0; q < 16; ++q) KQ_WRITE(q, 0);
+  }
+  if constexpr (NSET == 2) {
+    constexpr int SET_ = 1;
 #pragma unroll
-  for (int q = 0; q < 16; ++q) KQ_LOAD(q, 1);
+    for (int q = 0; q < 16; ++q) KQ_LOAD(q, min(1, nk - 1));
+  }
+  {
+    constexpr int SET_ = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) KQ_LOAD(q, min(NSET, nk - 1));
+  }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_s_barrier();
   // in the order the loop's last step reads them, so that the first MFMAs wait on a partial LDS count in every
@@ -1010,14 +1026,39 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
       KQ_READC(F0, KQ_ORDER(x), c, 0, 0);
       KQ_FENCE();
     }
-  for (int kt = 0; kt < nk; ++kt) {
-    const int ls = min(kt + 2, nk - 1);
-    if constexpr (NS == 4) {
+  // slice kt writes slice kt + 1 from set (kt + 1) % NSET and reloads that set with slice kt + 1 + NSET
+  if constexpr (NS == 4) {
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      {
+        constexpr int SET_ = 1;
+        const int ls = min(kt + 3, nk - 1);
+        KQ_STEP(F0, F1, 0, kt, ls);
+        KQ_STEP(F1, F0, 1, kt, ls);
+        KQ_STEP(F0, F1, 2, kt, ls);
+        KQ_STEP3(F1, F0, kt, ls);
+      }
+      {
+        constexpr int SET_ = 0;
+        const int ls = min(kt + 4, nk - 1);
+        KQ_STEP(F0, F1, 0, kt + 1, ls);
+        KQ_STEP(F1, F0, 1, kt + 1, ls);
+        KQ_STEP(F0, F1, 2, kt + 1, ls);
+        KQ_STEP3(F1, F0, kt + 1, ls);
+      }
+    }
+    if (kt < nk) {
+      constexpr int SET_ = 1;
+      const int ls = nk - 1;
       KQ_STEP(F0, F1, 0, kt, ls);
       KQ_STEP(F1, F0, 1, kt, ls);
       KQ_STEP(F0, F1, 2, kt, ls);
       KQ_STEP3(F1, F0, kt, ls);
-    } else {
+    }
+  } else {
+    constexpr int SET_ = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      const int ls = min(kt + 2, nk - 1);
       KQ8_STEP0(F0, F1, kt, ls);
       KQ8_STEP1(F1, F0, kt, ls);
     }
