@@ -51,21 +51,25 @@ int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind
 /* C[m, n] = epilogue(sum_k A[m, k] * B[k, n]), A: M x K, B: K x N (the NN form), C: M x N, bf16 or f16 operands;
  * out_kind and the epilogue as for krn_gemm_nt. Replaces krn's own GEMM tile program `acc += a[rows, ks] @
  * b[ks, cols]` (reference examples/04_libraries/01_gemm_tiles.py:34-40) and the multiply of lib.matmul
- * (src/krn/lib/lib_kernels.py:31-48), whose B operand is K x N. B is transposed into `workspace` (at least
+ * (src/krn/lib/lib_kernels.py:31-48), whose B operand is K x N. Products of at least 128 tiles of 256 x 256 with
+ * N % 256 == 0, K % 64 == 0, K >= 128 and 16-byte aligned operands read B K-major as it lies and leave `workspace`
+ * untouched (it may then be NULL). Any other B is transposed into `workspace` (at least
  * krn_gemm_nn_workspace(n, k) bytes of device memory, owned by the caller) and the NT kernels run on it; the
  * workspace must not be touched by other work until this call's work on `stream` has run. */
 int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n, int64_t k,
                 int nops, const int* ops, const float* scalars, const void* const* vectors, void* workspace,
                 int64_t workspace_bytes, void* stream);
 
-/* Bytes of workspace krn_gemm_nn needs for an N-column, K-row B operand (n * k 16-bit elements). */
+/* Bytes of workspace krn_gemm_nn may need for an N-column, K-row B operand (n * k 16-bit elements; the products
+ * that read B as it lies need none). */
 int64_t krn_gemm_nn_workspace(int64_t n, int64_t k);
 
 /* krn_gemm_nn without a workspace and without any allocation: the transposed B operand goes to a device array the
  * library holds (64 MiB per GPU it runs on, kept until the process ends; krn_gemm_nn_noalloc_limit() returns the
  * size). This entry point has no counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc,
- * hipFree or allocating library routine; it refuses a B whose n * k * 2 bytes exceed the limit. The array is looked
+ * hipFree or allocating library routine; it refuses a B whose n * k * 2 bytes exceed the limit when the product
+ * needs the transposed copy (the products krn_gemm_nn reads B as it lies for use no scratch). The array is looked
  * up once per device (hipGetSymbolAddress) on that device's first call, with the stream's device current. Every call
  * on one GPU shares that GPU's array: calls that overlap on one GPU (concurrent streams, or another host thread)
  * race and must be ordered by the caller. */

@@ -49,6 +49,8 @@ __device__ __forceinline__ float activation(int op, float x) {
 
 enum Format : int { FMT_BF16 = 0, FMT_F16 = 1, FMT_I8 = 2, FMT_FP8 = 3 };
 
+typedef short v4s16 __attribute__((ext_vector_type(4)));  // the result type of ds_read_b64_tr_b16
+
 template <int FMT>
 struct Mfma;
 
@@ -851,7 +853,12 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
 // bf16 8192^3: 3-5 % faster than the eight-wave ring with direct-to-LDS slices, whose loads cost about a sixth of its
 // loop in LDS bandwidth (eight waves of 64 x 128 read 96 KiB of fragments per 64-byte slice, four of 128 x 128 read
 // 64 KiB per 128-byte slice).
-template <int FMT>
+//
+// NN: B is stored K x N (row k of B is `ldb` bytes apart, N a multiple of 256, 16-bit elements): a slice of B is 64
+// rows of 512 bytes kept in LDS as [k][n] with 16-byte chunk c of row k at slot c ^ 4 (k & 3), and every B fragment
+// is two transposed reads (ds_read_b64_tr_b16) that hand lane L column n = L & 31 of its block and the same eight
+// k as the lane's A fragment holds. No transposed copy of B is made.
+template <int FMT, bool NN = false>
 __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
                                                     void* __restrict__ C, int64_t M, int64_t N, int64_t kbytes,
                                                     int64_t lda, int64_t ldb, int64_t ldc, Epilogue e) {
@@ -877,9 +884,12 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
     return (const void*)(((uint64_t)hi << 32) | lo);
   };
   const int64_t a_bytes = __builtin_amdgcn_readfirstlane((int)min((M - m0) * lda, (int64_t)0x7fffffff));
-  const int64_t b_bytes = __builtin_amdgcn_readfirstlane((int)min((N - n0) * ldb, (int64_t)0x7fffffff));
+  static_assert(!NN || CH == 1, "NN: 16-bit operands");
+  // NN: the panel is columns n0 .. n0 + 255 of every row of B (the host checks that it is addressable)
+  const int64_t b_bytes = __builtin_amdgcn_readfirstlane(
+      NN ? (int)((kbytes / 2 - 1) * ldb + BN * 2) : (int)min((N - n0) * ldb, (int64_t)0x7fffffff));
   const __amdgpu_buffer_rsrc_t a_rsrc = panel_rsrc(uniform(A + m0 * lda), a_bytes),
-                              b_rsrc = panel_rsrc(uniform(B + n0 * ldb), b_bytes);
+                              b_rsrc = panel_rsrc(uniform(B + (NN ? n0 * 2 : n0 * ldb)), b_bytes);
   // wave w stages rows 64 w .. 64 w + 63 of A and of B, 8 rows (1 KiB) per load; lane i takes row i / 8 and the
   // global chunk that belongs at slot i % 8
   const int lrow = lane >> 3, lslot = lane & 7;
@@ -889,7 +899,26 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
     const int row = wave * 64 + j * 8 + lrow;
     ga[j] = (uint32_t)(row * lda + ((lslot ^ swz8(row)) * 16));
     gb[j] = (uint32_t)(row * ldb + ((lslot ^ swz8(row)) * 16));
+    if constexpr (NN) {
+      // wave w stages k rows 16 w .. 16 w + 15 of the slice, two 512-byte rows per load; lane i takes row i / 32 and
+      // the chunk that belongs at slot i % 32
+      const int krow = wave * 16 + j * 2 + (lane >> 5), slot = lane & 31;
+      gb[j] = (uint32_t)(krow * ldb + ((slot ^ (4 * (krow & 3))) * 16));
+    }
   }
+  // NN: per lane, the byte offset in a stage's B part of its transposed reads for block j at step 0 (the key rows
+  // (g / 2) 8 + (a16 / 4) and + 4, columns 32 j + (g % 2) 16 + 4 (a16 % 4) of this wave's 128, g = lane / 16)
+  int trb[4] = {0, 0, 0, 0};
+  if constexpr (NN) {
+    const int g = lane >> 4, a16 = lane & 15;
+    const int krow = (g >> 1) * 8 + (a16 >> 2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = wn * 128 + j * 32 + (g & 1) * 16 + 4 * (a16 & 3);
+      trb[j] = krow * 512 + (((n >> 3) ^ (4 * (krow & 3))) * 16) + (n & 7) * 2;
+    }
+  }
+  const int b_step = NN ? 64 * (int)ldb : BKB;  // bytes from one slice of B to the next
   // fragment of MFMA step s: chunks (2 s + half) CH + c of row r32 of a 32-row block (the swizzle depends on r32 only)
   const int sw = (r32 >> 1) & 7;
   int rd[NS][CH];
@@ -917,14 +946,25 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
     if ((q) < 8)                                                                                               \
       stg[SET_][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ga[(q) & 7], (slice) * BKB, 0)); \
     else                                                                                                       \
-      stg[SET_][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, gb[(q) & 7], (slice) * BKB, 0)); \
+      stg[SET_][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, gb[(q) & 7], (slice) * b_step, 0)); \
   } while (0)
 #define KQ_WRITE(q, slice)                                                                                     \
   *reinterpret_cast<u32x4*>(lds + ((slice) & 1) * STAGE + ((q) < 8 ? 0 : BM * BKB) + wr + ((q) & 7) * 1024) = stg[SET_][q]
 #define KQ_READC(F, r, c, slice, s)                                                                            \
-  F[(r) * CH + (c)] = *reinterpret_cast<const u32x4*>(                                                         \
-      lds + ((slice) & 1) * STAGE + rd[s][c] +                                                                 \
-      ((r) < 4 ? (wm * 128 + (r) * 32) * 128 : BM * BKB + (wn * 128 + ((r) - 4) * 32) * 128))
+  do {                                                                                                         \
+    if (NN && (r) >= 4) {                                                                                      \
+      const uint8_t* p = lds + ((slice) & 1) * STAGE + BM * BKB + trb[((r) - 4) & 3] + (s) * 16 * 512;          \
+      const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(                        \
+                        (__attribute__((address_space(3))) v4s16*)p));                                          \
+      const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(                        \
+                        (__attribute__((address_space(3))) v4s16*)(p + 4 * 512)));                              \
+      F[(r) * CH + (c)] = u32x4{lo[0], lo[1], hi[0], hi[1]};                                                   \
+    } else {                                                                                                   \
+      F[(r) * CH + (c)] = *reinterpret_cast<const u32x4*>(                                                     \
+          lds + ((slice) & 1) * STAGE + rd[s][c] +                                                             \
+          ((r) < 4 ? (wm * 128 + (r) * 32) * 128 : BM * BKB + (wn * 128 + ((r) - 4) * 32) * 128));             \
+    }                                                                                                          \
+  } while (0)
 #define KQ_FENCE() __builtin_amdgcn_sched_barrier(0)
 #define KQ_READ(F, r, slice, s) KQ_READC(F, r, 0, slice, s)
 #define KQ_MMA(F, m) Unit::step(acc[(m) >> 2][(m) & 3], &F[((m) >> 2) * CH], &F[(4 + ((m) & 3)) * CH])
@@ -942,15 +982,16 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
       if (m % 4 == 3) { KQ_LOAD((s) * 4 + m / 4, ls); KQ_FENCE(); }                                           \
     }                                                                                                          \
   } while (0)
-  // step 3: items 12-15 written and reloaded under the first eight MFMAs, then the barrier (this wave's LDS
-  // traffic done), then the first fragments of slice kt + 1 under the last eight
+  // step 3: items 12-15 written under the first four MFMAs and reloaded under the next four, then the barrier
+  // (this wave's LDS traffic done, its last write four MFMAs old), then the first fragments of slice kt + 1 under
+  // the last eight
 #define KQ_STEP3(CUR, NXT, kt, ls)                                                                             \
   do {                                                                                                         \
     _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
       KQ_MMA(CUR, m);                                                                                          \
       KQ_FENCE();                                                                                              \
-      if (m < 8 && m % 2 == 0) { KQ_WRITE(12 + m / 2, (kt) + 1); KQ_FENCE(); }                                 \
-      if (m < 8 && m % 2 == 1) { KQ_LOAD(12 + m / 2, ls); KQ_FENCE(); }                                        \
+      if (m < 4) { KQ_WRITE(12 + m, (kt) + 1); KQ_FENCE(); }                                                   \
+      if (m >= 4 && m < 8) { KQ_LOAD(8 + m, ls); KQ_FENCE(); }                                                 \
       if (m == 7) {                                                                                            \
         __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0), vmcnt and expcnt left alone */                     \
         __builtin_amdgcn_s_barrier();                                                                          \
@@ -960,7 +1001,7 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
     }                                                                                                          \
   } while (0)
   // fp8 (two steps of 64-cycle MFMAs per slice). Step 0: after MFMA m the next step's fragment chunk m (of
-  // KQ_ORDER(m / 2)), then item m / 2 of slice kt + 1 written (m even) or reloaded with slice `ls` (m odd).
+  // KQ_ORDER(m / 2)), item m of slice kt + 1 written (m < 12) and item m - 2 reloaded with slice `ls`.
 #define KQ8_STEP0(CUR, NXT, kt, ls)                                                                            \
   do {                                                                                                         \
     _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
@@ -968,19 +1009,18 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
       KQ_FENCE();                                                                                              \
       KQ_READC(NXT, KQ_ORDER(m / 2), m % 2, kt, 1);                                                            \
       KQ_FENCE();                                                                                              \
-      if (m % 2 == 0) KQ_WRITE(m / 2, (kt) + 1); else KQ_LOAD(m / 2, ls);                                      \
-      KQ_FENCE();                                                                                              \
+      if (m < 12) { KQ_WRITE(m, (kt) + 1); KQ_FENCE(); }                                                       \
+      if (m >= 2 && m < 14) { KQ_LOAD(m - 2, ls); KQ_FENCE(); }                                                \
     }                                                                                                          \
   } while (0)
-  // step 1: items 8-15 written under the first seven MFMAs, the barrier after the eighth, then the first step's
-  // fragments of slice kt + 1 (two chunks per MFMA) and the reloads of items 8-15
+  // step 1: items 12-15 written under the first four MFMAs, the barrier after the eighth, then the first step's
+  // fragments of slice kt + 1 (two chunks per MFMA) and the reloads of items 12-15
 #define KQ8_STEP1(CUR, NXT, kt, ls)                                                                            \
   do {                                                                                                         \
     _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
       KQ_MMA(CUR, m);                                                                                          \
       KQ_FENCE();                                                                                              \
-      if (m < 7) { KQ_WRITE(8 + m, (kt) + 1); KQ_FENCE(); }                                                    \
-      if (m == 6) { KQ_WRITE(15, (kt) + 1); KQ_FENCE(); }                                                      \
+      if (m < 4) { KQ_WRITE(12 + m, (kt) + 1); KQ_FENCE(); }                                                   \
       if (m == 7) {                                                                                            \
         __builtin_amdgcn_s_waitcnt(0xc07f);                                                                    \
         __builtin_amdgcn_s_barrier();                                                                          \
@@ -990,12 +1030,10 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
         KQ_READC(NXT, KQ_ORDER(m - 7), 0, (kt) + 1, 0);                                                        \
         KQ_READC(NXT, KQ_ORDER(m - 7), 1, (kt) + 1, 0);                                                        \
         KQ_FENCE();                                                                                            \
-        KQ_LOAD(8 + m - 7, ls);                                                                                \
-        KQ_FENCE();                                                                                            \
+        if (m < 11) { KQ_LOAD(12 + m - 7, ls); KQ_FENCE(); }                                                   \
       }                                                                                                        \
     }                                                                                                          \
   } while (0)
-
   {
     // slice 0 through set 0 into stage 0; slices 1 .. NSET into the sets (set of slice j: j % NSET)
     constexpr int SET_ = 0;
@@ -1591,16 +1629,14 @@ static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t
 
 extern "C" int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void* stream);
 
-extern "C" {
-
-// See include/krn_amd.h for the contract of each entry point.
-int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n, int64_t k,
-                int nops, const int* ops, const float* scalars, const void* const* vectors, void* stream) {
-  Epilogue e{};
+// The epilogue chain of a launch, checked: at most four known operations, a vector for every per-row or per-column
+// one. `who` prefixes the error message.
+static bool epilogue_of(Epilogue& e, int out_kind, int nops, const int* ops, const float* scalars,
+                        const void* const* vectors, const char* who) {
   e.out_kind = out_kind;
   if (nops < 0 || nops > 4) {
-    krn_set_error("gemm: %d epilogue operations, at most 4", nops);
-    return -1;
+    krn_set_error("%s: %d epilogue operations, at most 4", who, nops);
+    return false;
   }
   e.nops = nops;
   for (int i = 0; i < nops; ++i) {
@@ -1609,14 +1645,24 @@ int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind
     e.vec[i] = vectors ? vectors[i] : nullptr;
     const int op = ops[i] & ((1 << VEC_KIND_SHIFT) - 1), kind = ops[i] >> VEC_KIND_SHIFT;
     if (ops[i] < 0 || op > SILU || kind > 2 || (kind != 0 && (op >= RELU || op % 3 == 0))) {
-      krn_set_error("gemm: unknown epilogue operation %d", ops[i]);
-      return -1;
+      krn_set_error("%s: unknown epilogue operation %d", who, ops[i]);
+      return false;
     }
     if (op < RELU && op % 3 != 0 && e.vec[i] == nullptr) {
-      krn_set_error("gemm: epilogue operation %d needs a vector", i);
-      return -1;
+      krn_set_error("%s: epilogue operation %d needs a vector", who, i);
+      return false;
     }
   }
+  return true;
+}
+
+extern "C" {
+
+// See include/krn_amd.h for the contract of each entry point.
+int krn_gemm_nt(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n, int64_t k,
+                int nops, const int* ops, const float* scalars, const void* const* vectors, void* stream) {
+  Epilogue e{};
+  if (!epilogue_of(e, out_kind, nops, ops, scalars, vectors, "gemm")) return -1;
   if (m < 0 || n < 0 || k < 0) {
     krn_set_error("gemm: negative extent");
     return -1;
@@ -1663,6 +1709,15 @@ __global__ __launch_bounds__(256) void transpose16(const uint16_t* __restrict__ 
 
 // The NN product `a[rows, ks] @ b[ks, cols]` with B stored K x N: B is transposed into `bt` (N x K, n * k 16-bit
 // elements) and the NT kernels run on it. Both launches go on `stream`, in that order.
+// The NN products the four-wave loop takes with B read K-major from LDS (no transposed copy): at least 128 tiles
+// of 256 x 256, N a multiple of 256, K of 64 (whole 128-byte slices, at least two), 16-byte aligned operands, and
+// panels addressable by 31-bit buffer offsets.
+static bool nn_direct(const void* a, const void* b, int64_t m, int64_t n, int64_t k) {
+  const int64_t t256 = ((m + 255) / 256) * (n / 256);
+  return m > 0 && n > 0 && n % 256 == 0 && k % 64 == 0 && k >= 128 && t256 >= 128 && (uintptr_t)a % 16 == 0 &&
+         (uintptr_t)b % 16 == 0 && 256 * k * 2 <= 0x7fffffff && (k - 1) * n * 2 + 512 <= 0x7fffffff;
+}
+
 static int gemm_nn_through(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n,
                            int64_t k, int nops, const int* ops, const float* scalars, const void* const* vectors,
                            void* bt, void* stream) {
@@ -1672,6 +1727,31 @@ static int gemm_nn_through(int in_kind, const void* a, const void* b, void* c, i
   }
   if (m < 0 || n < 0 || k < 0) {
     krn_set_error("gemm_nn: negative extent");
+    return -1;
+  }
+  if (nn_direct(a, b, m, n, k)) {
+    Epilogue e{};
+    if (!epilogue_of(e, out_kind, nops, ops, scalars, vectors, "gemm_nn")) return -1;
+    if (out_kind != F32 && out_kind != F16 && out_kind != BF16) {
+      krn_set_error("gemm_nn: output kind %d is not stored by the tile GEMM", out_kind);
+      return -1;
+    }
+    const int64_t tiles = ((m + 255) / 256) * (n / 256);
+    if (in_kind == BF16)
+      hipLaunchKernelGGL((gemm_quad<FMT_BF16, true>), dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
+                         (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n, e);
+    else
+      hipLaunchKernelGGL((gemm_quad<FMT_F16, true>), dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
+                         (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n, e);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+      krn_set_error("gemm_nn launch: %s", hipGetErrorString(err));
+      return (int)err;
+    }
+    return 0;
+  }
+  if (bt == nullptr && n > 0 && k > 0) {
+    krn_set_error("gemm_nn: this product needs the transposed operand's workspace");
     return -1;
   }
   if (n > 0 && k > 0) {
@@ -1686,7 +1766,7 @@ extern "C" int64_t krn_gemm_nn_workspace(int64_t n, int64_t k) { return n < 0 ||
 extern "C" int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n,
                            int64_t k, int nops, const int* ops, const float* scalars, const void* const* vectors,
                            void* workspace, int64_t workspace_bytes, void* stream) {
-  const int64_t need = krn_gemm_nn_workspace(n, k);
+  const int64_t need = nn_direct(a, b, m, n, k) ? 0 : krn_gemm_nn_workspace(n, k);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     krn_set_error("gemm_nn: the workspace holds %lld bytes, the transposed operand needs %lld",
                   (long long)workspace_bytes, (long long)need);
@@ -1731,7 +1811,7 @@ extern "C" int64_t krn_gemm_nn_noalloc_limit(void) { return KRN_NN_SCRATCH_BYTES
 extern "C" int krn_gemm_nn_noalloc(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m,
                                    int64_t n, int64_t k, int nops, const int* ops, const float* scalars,
                                    const void* const* vectors, void* stream) {
-  const int64_t need = krn_gemm_nn_workspace(n, k);
+  const int64_t need = nn_direct(a, b, m, n, k) ? 0 : krn_gemm_nn_workspace(n, k);
   if (need > KRN_NN_SCRATCH_BYTES) {
     krn_set_error("gemm_nn_noalloc: B of %lld x %lld needs %lld bytes of scratch; the library holds %lld "
                   "(use krn_gemm_nn with a workspace)", (long long)k, (long long)n, (long long)need,

@@ -1,14 +1,17 @@
 """krn_gemm_nn, the NN product of krn's own GEMM example (reference examples/04_libraries/01_gemm_tiles.py:34-40,
-B stored K x N), through the C ABI: it transposes B into the caller's workspace and runs the NT kernels, so its
-result is bit-identical to krn_gemm_nt on B transposed on the host; a workspace that is too small is refused before
-anything is enqueued."""
+B stored K x N), through the C ABI. Large products with N % 256 == 0 and K % 64 == 0 read B K-major as it lies
+(transposed LDS reads), the others transpose B into the caller's workspace and run the NT kernels; either way the
+result is bit-identical to krn_gemm_nt on B transposed on the host, because every lane pairs the same k in the same
+order. A workspace that is too small is refused before anything is enqueued when the product needs one."""
 
+
+import ctypes
 
 import numpy as np
 import pytest
 
 from krn_amd import T
-from krn_amd.dtypes import BF16, F16
+from krn_amd.dtypes import BF16, F16, F32
 from krn_amd.runtime import library
 from oracle.numerics import bf16_words
 
@@ -39,6 +42,49 @@ def test_gemm_nn_equals_gemm_nt_on_the_transposed_operand(device, dtype, m, n, k
                                             library.kind(dtype), m, n, k, 0, None, None, None, workspace.pointer,
                                             need, stream), "krn_gemm_nn")
     nt(device, dtype, a, bt, m, n, k, c_nt)
+    np.testing.assert_array_equal(c_nn.to_host(), c_nt.to_host())
+
+
+def operands(device, dtype, m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    x, y = rng.standard_normal((m, k)).astype(np.float32), rng.standard_normal((k, n)).astype(np.float32)
+    if dtype == BF16:
+        ah, bh, kind = bf16_words(x), bf16_words(y), T.bf16
+    else:
+        ah, bh, kind = x.astype(np.float16), y.astype(np.float16), T.f16
+    return device.to_device(ah, kind), device.to_device(bh, kind), device.to_device(np.ascontiguousarray(bh.T), kind), kind
+
+
+# the direct shapes: at least 128 tiles of 256 x 256; whole and ragged M, an odd number of 128-byte K slices
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 512), (2000, 4096, 384), (4096, 2048, 192)])
+def test_gemm_nn_reading_b_as_it_lies_needs_no_workspace(device, dtype, m, n, k):
+    a, b, bt, kind = operands(device, dtype, m, n, k, m + n + k)
+    c_nn, c_nt = device.empty(kind, m, n), device.empty(kind, m, n)
+    library.check(library.lib().krn_gemm_nn(library.kind(dtype), a.pointer, b.pointer, c_nn.pointer,
+                                            library.kind(dtype), m, n, k, 0, None, None, None, None, 0,
+                                            device.default_stream.handle), "krn_gemm_nn")
+    nt(device, dtype, a, bt, m, n, k, c_nt)
+    np.testing.assert_array_equal(c_nn.to_host(), c_nt.to_host())
+
+
+def test_gemm_nn_direct_with_bias_and_activation(device):
+    m, n, k = 2048, 4096, 256
+    a, b, bt, kind = operands(device, BF16, m, n, k, 7)
+    bias = device.to_device(np.random.default_rng(8).standard_normal(n).astype(np.float32), T.f32)
+    ops = [library.ADD_COL, library.GELU]
+    c_nn, c_nt = device.empty(T.f32, m, n), device.empty(T.f32, m, n)
+    n_ops = len(ops)
+    codes = (ctypes.c_int * n_ops)(*ops)
+    scalars = (ctypes.c_float * n_ops)(0.0, 0.0)
+    vectors = (ctypes.c_void_p * n_ops)(bias.pointer, None)
+    stream = device.default_stream.handle
+    library.check(library.lib().krn_gemm_nn(library.kind(BF16), a.pointer, b.pointer, c_nn.pointer,
+                                            library.kind(F32), m, n, k, n_ops, codes, scalars, vectors, None, 0,
+                                            stream), "krn_gemm_nn")
+    library.check(library.lib().krn_gemm_nt(library.kind(BF16), a.pointer, bt.pointer, c_nt.pointer,
+                                            library.kind(F32), m, n, k, n_ops, codes, scalars, vectors, stream),
+                  "krn_gemm_nt")
     np.testing.assert_array_equal(c_nn.to_host(), c_nt.to_host())
 
 
