@@ -348,9 +348,10 @@ __device__ __forceinline__ void direct_vectors(DirectVectors<TM, TN>& dv, const 
   }
 }
 
-template <bool INT, int TM, int TN, typename V>
+template <bool INT, bool BF, int TM, int TN, typename V>
 __device__ __forceinline__ void store_block_direct(const V& block, const DirectVectors<TM, TN>& dv, int i, int j,
-                                                   uint16_t* lane_out, int64_t ldc, const Epilogue& e, int lane) {
+                                                   __amdgpu_buffer_rsrc_t out, uint32_t lane_off, int64_t ldc,
+                                                   const Epilogue& e, int lane) {
   float v[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) v[r] = INT ? (float)(int32_t)block[r] : (float)block[r];
@@ -373,18 +374,18 @@ __device__ __forceinline__ void store_block_direct(const V& block, const DirectV
     }
   }
   const int odd = lane & 1;
-  const bool bf = e.out_kind == BF16;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const float send = odd ? v[2 * k] : v[2 * k + 1];
     // quad_perm [1, 0, 3, 2]: exchange with lane ^ 1
     const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, true));
     const float lo = odd ? recv : v[2 * k], hi = odd ? v[2 * k + 1] : recv;
-    const uint32_t pair = bf ? f2bf2(lo, hi) : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
+    const uint32_t pair = BF ? f2bf2(lo, hi) : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
     // accumulator register 2k + odd holds row ((2k + odd) >> 2) * 8 + half * 4 + ((2k + odd) & 3); the lane's part
-    // (half * 4 + odd) is in lane_out, the rest is the same for the whole wave
-    const int64_t step = (int64_t)((k >> 1) * 8 + (k & 1) * 2) + (int64_t)(i * 32);
-    __builtin_nontemporal_store(pair, reinterpret_cast<uint32_t*>(lane_out + step * ldc + j * 32));
+    // (half * 4 + odd) is in lane_off, the rest is the same for the whole wave: a scalar offset
+    const int step = (k >> 1) * 8 + (k & 1) * 2 + i * 32;
+    const int soff = __builtin_amdgcn_readfirstlane((int)(((int64_t)step * ldc + j * 32) * 2));
+    __builtin_amdgcn_raw_buffer_store_b32(pair, out, (int)lane_off, soff, 2 /* nt */);
   }
 }
 
@@ -408,22 +409,34 @@ __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* p
                                            int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
                                            int lane) {
   const bool direct = direct_epilogue(e) && (ldc % 2) == 0 && (uintptr_t)C % 4 == 0 && row0 + 32 * TM <= M &&
-                      col0 + 32 * TN <= N;
+                      col0 + 32 * TN <= N && (int64_t)32 * TM * ldc * 2 <= 0x7fffffff;
   if (direct) {
     DirectVectors<TM, TN> dv;
     direct_vectors(dv, e, row0, col0, lane);
-    // each lane stores a column pair at (c & ~1) of rows half * 4 + odd + wave-uniform steps
+    // the wave's region of C as a buffer resource; each lane stores a column pair at (c & ~1) of rows
+    // half * 4 + odd, plus wave-uniform steps
     const int c = lane & 31;
-    uint16_t* lane_out = static_cast<uint16_t*>(C) + (row0 + (lane >> 5) * 4 + (c & 1)) * ldc + col0 + (c & ~1);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        if constexpr (AGPR)
-          store_block_direct<INT>(agpr_block(acc[i][j]), dv, i, j, lane_out, ldc, e, lane);
-        else
-          store_block_direct<INT>(acc[i][j], dv, i, j, lane_out, ldc, e, lane);
-      }
+    // (readfirstlane returns int: each word goes through uint32_t, so the low word is never sign-extended into
+    // the high one)
+    const uint64_t base = (uint64_t)(static_cast<uint16_t*>(C) + row0 * ldc + col0);
+    const uint32_t base_lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
+    const uint32_t base_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+    const void* region = (const void*)(((uint64_t)base_hi << 32) | (uint64_t)base_lo);
+    const __amdgpu_buffer_rsrc_t out = panel_rsrc(region, (int64_t)32 * TM * ldc * 2);
+    const uint32_t lane_off = (uint32_t)((((lane >> 5) * 4 + (c & 1)) * ldc + (c & ~1)) * 2);
+#define KRN_DIRECT(BF)                                                                                       \
+  _Pragma("unroll") for (int i = 0; i < TM; ++i) _Pragma("unroll") for (int j = 0; j < TN; ++j) {            \
+    if constexpr (AGPR)                                                                                      \
+      store_block_direct<INT, BF>(agpr_block(acc[i][j]), dv, i, j, out, lane_off, ldc, e, lane);            \
+    else                                                                                                     \
+      store_block_direct<INT, BF>(acc[i][j], dv, i, j, out, lane_off, ldc, e, lane);                         \
+  }
+    if (e.out_kind == BF16) {
+      KRN_DIRECT(true)
+    } else {
+      KRN_DIRECT(false)
+    }
+#undef KRN_DIRECT
     return;
   }
   // The out-of-line store takes the epilogue by address. Passing the kernel argument itself would copy it to private
@@ -474,7 +487,8 @@ __device__ __forceinline__ int swz4(int row) { return (row >> 2) & 3; }
 // first regrouped per XCD (each XCD gets one contiguous range of tiles and its own L2 sees a compact panel), then
 // ordered in groups of GROUP_M tile rows so neighbours share A rows and B columns.
 __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int& tm, int& tn) {
-  constexpr int GROUP_M = 4;  // bf16 8192^3: 0.5-1.5 % faster than 8 (2: -6 %, 6: -1 %, 16: -9 %); fp8 equal
+  constexpr int GROUP_M = 4;  // bf16 8192^3: 0.5-1.5 % faster than 8 (2: -6 %, 6: -1 %, 16: -9 %); fp8 equal; the
+                              // four-wave loop: 8 equal, 2 -1.5 %
   int nb = tiles_m * tiles_n;
   int bid = blockIdx.x;
   if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
@@ -966,6 +980,7 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
     }                                                                                                          \
   } while (0)
 #define KQ_FENCE() __builtin_amdgcn_sched_barrier(0)
+#define KQ_BARRIER() __builtin_amdgcn_s_barrier()
 #define KQ_READ(F, r, slice, s) KQ_READC(F, r, 0, slice, s)
 #define KQ_MMA(F, m) Unit::step(acc[(m) >> 2][(m) & 3], &F[((m) >> 2) * CH], &F[(4 + ((m) & 3)) * CH])
   // fragments in the order the next step's MFMAs use them: A0 B0 B1 B2 B3 A1 A2 A3
@@ -994,7 +1009,7 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
       if (m >= 4 && m < 8) { KQ_LOAD(8 + m, ls); KQ_FENCE(); }                                                 \
       if (m == 7) {                                                                                            \
         __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0), vmcnt and expcnt left alone */                     \
-        __builtin_amdgcn_s_barrier();                                                                          \
+        KQ_BARRIER();                                                                                          \
         KQ_FENCE();                                                                                            \
       }                                                                                                        \
       if (m >= 7 && m < 15) { KQ_READ(NXT, KQ_ORDER(m - 7), (kt) + 1, 0); KQ_FENCE(); }                       \
@@ -1108,6 +1123,7 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
 #undef KQ8_STEP0
 #undef KQ8_STEP1
 #undef KQ_FENCE
+#undef KQ_BARRIER
 #undef KQ_MMA
 #undef KQ_ORDER
 #undef KQ_STEP

@@ -10,6 +10,8 @@ import numpy as np
 import pytest
 
 from krn_amd import T
+from krn_amd.dtypes import BF16, I8
+from krn_amd.runtime import hipapi, library
 from oracle.numerics import bf16_values, bf16_words, e4m3_decode, e4m3_encode
 from tests.helpers import agree_bound
 from tests.kernels import tile_programs as programs
@@ -101,3 +103,37 @@ def test_int8_gemm_over_the_full_int8_range_is_bit_exact(device, m, n, k):
     c = device.empty(T.i32, m, n)
     programs.gemm_i8_i32[TILING](device.to_device(a), device.to_device(b), c)
     np.testing.assert_array_equal(c.to_host(), a.astype(np.int64) @ b.astype(np.int64).T)
+
+
+# one shape per kernel family whose whole blocks take the direct store: the mid-size pipeline (512^3), the
+# four-wave whole-tile loop (4096 x 4096 x 256) and the eight-wave int8 pipeline (W8A8-like dequantisation)
+@pytest.mark.parametrize("m,n,k,dtype", [(512, 512, 512, BF16), (4096, 4096, 256, BF16), (4096, 4096, 256, I8)])
+def test_direct_store_at_an_address_whose_low_word_has_bit_31_set(device, m, n, k, dtype):
+    """Regression: the direct epilogue stores through a buffer resource built from the two 32-bit words of C's
+    address; a low word with bit 31 set was once sign-extended into the high word (a memory fault). Here C lies at
+    such an address, and its result must equal the same product into an ordinary allocation bit for bit."""
+    rng = np.random.default_rng(m + k)
+    if dtype == I8:
+        a = device.to_device(rng.integers(-127, 128, (m, k), dtype=np.int8))
+        b = device.to_device(rng.integers(-127, 128, (n, k), dtype=np.int8))
+        sa = device.to_device(rng.uniform(0.5, 2.0, m).astype(np.float32))
+        sb = device.to_device(rng.uniform(0.5, 2.0, n).astype(np.float32))
+        ops = [(library.MUL_ROW, 0.0, sa.pointer), (library.MUL_COL, 0.0, sb.pointer)]
+    else:
+        a = device.to_device(bf16_words(rng.standard_normal((m, k)).astype(np.float32)), T.bf16)
+        b = device.to_device(bf16_words(rng.standard_normal((n, k)).astype(np.float32)), T.bf16)
+        ops = []
+    nbytes = m * n * 2
+    want = device.empty(T.bf16, m, n)
+    stream = device.default_stream.handle
+    library.gemm_nt(dtype, a.pointer, b.pointer, want.pointer, BF16, m, n, k, ops, stream)
+    arena = device.empty(T.u8, (1 << 31) + nbytes + 256)
+    low = arena.pointer & 0xFFFFFFFF
+    offset = 0 if low >= 0x80000000 else (0x80000000 - low + 255) // 256 * 256
+    target = arena.pointer + offset
+    assert target & 0x80000000 and offset + nbytes <= (1 << 31) + nbytes + 256
+    library.gemm_nt(dtype, a.pointer, b.pointer, target, BF16, m, n, k, ops, stream)
+    device.default_stream.sync()
+    got = np.empty((m, n), np.uint16)
+    hipapi.api().hipMemcpy(got.ctypes.data, target, nbytes, hipapi.D2H)
+    np.testing.assert_array_equal(got, want.to_host())
