@@ -303,10 +303,9 @@ __device__ __forceinline__ void store_block(const V& block, uint32_t* patch, voi
 // patch, for epilogues of at most two operations that are float32 scalars or row/column vectors (no activation):
 // the headline bf16 product, the fp8 product's `acc * (scale_a * scale_b)`, the W8A8 dequantisation
 // `acc * scale_a[m] * scale_w[n]`. Lane L holds column c = L & 31 at rows R(r) = (r / 4) * 8 + (L / 32) * 4 + r % 4;
-// neighbouring lanes hold columns c and c ^ 1 of the same rows. One DPP swap per register pair (2i, 2i + 1) gives the
-// even lane both columns of row R(2i) and the odd lane both columns of row R(2i + 1), so every lane stores eight
-// 4-byte pairs and each store instruction writes 64-byte row segments. The operations and their rounding are the
-// patch path's, so the result is the same bit for bit.
+// neighbouring lanes hold columns c and c ^ 1 of the same rows. Blocks go out in pairs (store_pair_direct), so that
+// each store instruction writes whole 128-byte lines: non-temporal half lines cost a third more HBM writes. The
+// operations and their rounding are the patch path's, so the result is the same bit for bit.
 constexpr int DIRECT_OPS = 2;
 
 __device__ __forceinline__ bool direct_epilogue(const Epilogue& e) {
@@ -348,11 +347,11 @@ __device__ __forceinline__ void direct_vectors(DirectVectors<TM, TN>& dv, const 
   }
 }
 
-template <bool INT, bool BF, int TM, int TN, typename V>
-__device__ __forceinline__ void store_block_direct(const V& block, const DirectVectors<TM, TN>& dv, int i, int j,
-                                                   __amdgpu_buffer_rsrc_t out, uint32_t lane_off, int64_t ldc,
-                                                   const Epilogue& e, int lane) {
-  float v[16];
+// One block's 16 accumulators through the epilogue operations, in float32 (the patch path's operations and
+// rounding).
+template <bool INT, int TM, int TN, typename V>
+__device__ __forceinline__ void direct_ops(float (&v)[16], const V& block, const DirectVectors<TM, TN>& dv, int i,
+                                           int j, const Epilogue& e) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) v[r] = INT ? (float)(int32_t)block[r] : (float)block[r];
 #pragma unroll
@@ -373,17 +372,54 @@ __device__ __forceinline__ void store_block_direct(const V& block, const DirectV
       for (int r = 0; r < 16; ++r) v[r] = mul ? __fmul_rn(v[r], s) : __fadd_rn(v[r], s);
     }
   }
+}
+
+// One block (i, j): one DPP swap per register pair (2k, 2k + 1) gives the even lane both columns c, c + 1 of row
+// R(2k) and the odd lane both of row R(2k + 1); each store instruction writes 64-byte row segments (half lines).
+template <bool INT, bool BF, int TM, int TN, typename V>
+__device__ __forceinline__ void store_block_direct(const V& block, const DirectVectors<TM, TN>& dv, int i, int j,
+                                                   __amdgpu_buffer_rsrc_t out, uint32_t lane_off, int64_t ldc,
+                                                   const Epilogue& e, int lane) {
+  float v[16];
+  direct_ops<INT>(v, block, dv, i, j, e);
   const int odd = lane & 1;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const float send = odd ? v[2 * k] : v[2 * k + 1];
-    // quad_perm [1, 0, 3, 2]: exchange with lane ^ 1
     const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, true));
     const float lo = odd ? recv : v[2 * k], hi = odd ? v[2 * k + 1] : recv;
     const uint32_t pair = BF ? f2bf2(lo, hi) : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
-    // accumulator register 2k + odd holds row ((2k + odd) >> 2) * 8 + half * 4 + ((2k + odd) & 3); the lane's part
-    // (half * 4 + odd) is in lane_off, the rest is the same for the whole wave: a scalar offset
+    // register 2k + odd holds row ((2k + odd) >> 2) * 8 + half * 4 + ((2k + odd) & 3): the lane's part
+    // (half * 4 + odd) is in lane_off, the rest is a scalar offset
     const int step = (k >> 1) * 8 + (k & 1) * 2 + i * 32;
+    const int soff = __builtin_amdgcn_readfirstlane((int)(((int64_t)step * ldc + j * 32) * 2));
+    __builtin_amdgcn_raw_buffer_store_b32(pair, out, (int)lane_off, soff, 2 /* nt */);
+  }
+}
+
+// Blocks (i, j) and (i, j + 1), j even: 64 columns, one 128-byte line of 16-bit C per row. For every accumulator
+// register r (row R(r)) the even lane keeps its block-j value of column c and takes column c + 1 of block j from
+// lane c + 1, the odd lane keeps its block-(j + 1) value and takes column c - 1 of block j + 1 from lane c - 1 (one
+// DPP swap): the even lanes of a half-wave then hold block j of row R(r) and the odd lanes block j + 1, so each
+// 4-byte store instruction writes whole 128-byte lines (two rows), never a half line.
+template <bool INT, bool BF, int TM, int TN, typename V>
+__device__ __forceinline__ void store_pair_direct(const V& b0, const V& b1, const DirectVectors<TM, TN>& dv, int i,
+                                                  int j, __amdgpu_buffer_rsrc_t out, uint32_t lane_off, int64_t ldc,
+                                                  const Epilogue& e, int lane) {
+  float v0[16], v1[16];
+  direct_ops<INT>(v0, b0, dv, i, j, e);
+  direct_ops<INT>(v1, b1, dv, i, j + 1, e);
+  const int odd = lane & 1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float send = odd ? v0[r] : v1[r];
+    // quad_perm [1, 0, 3, 2]: exchange with lane ^ 1
+    const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, true));
+    const float lo = odd ? recv : v0[r], hi = odd ? v1[r] : recv;
+    const uint32_t pair = BF ? f2bf2(lo, hi) : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
+    // register r holds row (r >> 2) * 8 + half * 4 + (r & 3): the lane's part (half * 4, its column pair and
+    // block) is in lane_off, the rest is the same for the whole wave, a scalar offset
+    const int step = (r >> 2) * 8 + (r & 3) + i * 32;
     const int soff = __builtin_amdgcn_readfirstlane((int)(((int64_t)step * ldc + j * 32) * 2));
     __builtin_amdgcn_raw_buffer_store_b32(pair, out, (int)lane_off, soff, 2 /* nt */);
   }
@@ -423,13 +459,22 @@ __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* p
     const uint32_t base_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
     const void* region = (const void*)(((uint64_t)base_hi << 32) | (uint64_t)base_lo);
     const __amdgpu_buffer_rsrc_t out = panel_rsrc(region, (int64_t)32 * TM * ldc * 2);
-    const uint32_t lane_off = (uint32_t)((((lane >> 5) * 4 + (c & 1)) * ldc + (c & ~1)) * 2);
+    // AGPR (the four-wave loop): blocks in pairs, whole lines; the lane's row (half * 4) and its column pair
+    // (c & ~1) in block j (even lanes) or j + 1 (odd lanes). Otherwise block by block (measured 3 % faster for
+    // W8A8 on the eight-wave int8 loop, whose registers are tighter): row half * 4 + (c & 1), pair c & ~1.
+    const uint32_t lane_off = AGPR ? (uint32_t)((((lane >> 5) * 4) * ldc + (c & ~1) + (c & 1) * 32) * 2)
+                                   : (uint32_t)((((lane >> 5) * 4 + (c & 1)) * ldc + (c & ~1)) * 2);
+    static_assert(!AGPR || TN % 2 == 0, "blocks stored in pairs");
 #define KRN_DIRECT(BF)                                                                                       \
-  _Pragma("unroll") for (int i = 0; i < TM; ++i) _Pragma("unroll") for (int j = 0; j < TN; ++j) {            \
-    if constexpr (AGPR)                                                                                      \
-      store_block_direct<INT, BF>(agpr_block(acc[i][j]), dv, i, j, out, lane_off, ldc, e, lane);            \
-    else                                                                                                     \
-      store_block_direct<INT, BF>(acc[i][j], dv, i, j, out, lane_off, ldc, e, lane);                         \
+  _Pragma("unroll") for (int i = 0; i < TM; ++i) {                                                           \
+    if constexpr (AGPR) {                                                                                    \
+      _Pragma("unroll") for (int j = 0; j < TN; j += 2)                                                      \
+        store_pair_direct<INT, BF>(agpr_block(acc[i][j]), agpr_block(acc[i][j + 1]), dv, i, j, out,          \
+                                   lane_off, ldc, e, lane);                                                  \
+    } else {                                                                                                 \
+      _Pragma("unroll") for (int j = 0; j < TN; ++j)                                                         \
+        store_block_direct<INT, BF>(acc[i][j], dv, i, j, out, lane_off, ldc, e, lane);                       \
+    }                                                                                                        \
   }
     if (e.out_kind == BF16) {
       KRN_DIRECT(true)
