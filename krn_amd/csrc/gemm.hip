@@ -1612,7 +1612,7 @@ static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_
                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
   // bf16/f16 and fp8: four waves of 128 x 128 in a fixed instruction order (fp8 8192^3 7 % faster than the
   // eight-wave ping-pong, which keeps the one-slice K = 128 case). int8: eight waves (4 x 2, each 64 x 128 of the
-  // tile) that interleave their own LDS reads with their MFMAs (the four-wave loop measured 10 % slower on W8A8
+  // tile) that interleave their own LDS reads with their MFMAs (the four-wave loop measured 7-10 % slower on W8A8
   // M = 4096, whose K of 32 slices leaves more of the time to the prologue and epilogue).
   if constexpr (FMT == FMT_FP8) {
     if (kbytes >= 256) return launch_quad<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
