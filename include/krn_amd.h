@@ -64,6 +64,11 @@ int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, int out_kind
  * that read B as it lies need none). */
 int64_t krn_gemm_nn_workspace(int64_t n, int64_t k);
 
+/* Bytes of workspace this krn_gemm_nn call needs: 0 for a product that reads B as it lies (N % 256 == 0,
+ * K % 64 == 0, at least 128 tiles of 256 x 256, 16-byte aligned a and b), otherwise krn_gemm_nn_workspace(n, k).
+ * Like krn_gemm_nn_workspace, no counterpart in the reference: its NN products need no caller memory. */
+int64_t krn_gemm_nn_workspace_for(const void* a, const void* b, int64_t m, int64_t n, int64_t k);
+
 /* krn_gemm_nn without a workspace and without any allocation: the transposed B operand goes to a device array the
  * library holds (64 MiB per GPU it runs on, kept until the process ends; krn_gemm_nn_noalloc_limit() returns the
  * size). This entry point has no counterpart in the reference: it is for callers that cannot allocate device memory

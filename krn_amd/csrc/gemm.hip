@@ -1824,6 +1824,10 @@ static int gemm_nn_through(int in_kind, const void* a, const void* b, void* c, i
 
 extern "C" int64_t krn_gemm_nn_workspace(int64_t n, int64_t k) { return n < 0 || k < 0 ? 0 : n * k * 2; }
 
+extern "C" int64_t krn_gemm_nn_workspace_for(const void* a, const void* b, int64_t m, int64_t n, int64_t k) {
+  return nn_direct(a, b, m, n, k) ? 0 : krn_gemm_nn_workspace(n, k);
+}
+
 extern "C" int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n,
                            int64_t k, int nops, const int* ops, const float* scalars, const void* const* vectors,
                            void* workspace, int64_t workspace_bytes, void* stream) {

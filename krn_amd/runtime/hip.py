@@ -341,7 +341,11 @@ class Launch:
                 code = base + (1 if op.axis == "row" else 2) + library.VECTOR_KINDS[vector.dtype]
                 ops.append((code, 0.0, vector.pointer))
         if plan.layout == "nn":
-            need = library.gemm_nn_workspace(n, k)
+            need = library.gemm_nn_workspace_for(a.pointer, b.pointer, m, n, k)
+            if need == 0:  # B is read K x N as it lies: no workspace
+                direct = library.gemm_nn_call(plan.operand, a.pointer, b.pointer, c.pointer, plan.output, m, n, k,
+                                              ops, 0, 0)
+                return lambda stream: direct(stream.handle)
             scratch = StreamScratch(need)
             products: dict[int, Callable[[int], None]] = {}  # workspace pointer -> the product marshalled for it
 

@@ -47,6 +47,8 @@ def lib() -> ctypes.CDLL:
     ]  # fmt: skip
     handle.krn_gemm_nn_workspace.restype = c_int64
     handle.krn_gemm_nn_workspace.argtypes = [c_int64, c_int64]
+    handle.krn_gemm_nn_workspace_for.restype = c_int64
+    handle.krn_gemm_nn_workspace_for.argtypes = [c_void_p, c_void_p, c_int64, c_int64, c_int64]
     handle.krn_gemm_nn_noalloc.restype = c_int
     handle.krn_gemm_nn_noalloc.argtypes = [
         c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64, c_int, POINTER(c_int),
@@ -101,9 +103,15 @@ def gemm_nn_workspace(n: int, k: int) -> int:
     return lib().krn_gemm_nn_workspace(n, k)
 
 
+def gemm_nn_workspace_for(a: int, b: int, m: int, n: int, k: int) -> int:
+    """Bytes of workspace this NN product needs: 0 when the kernel reads B as it lies."""
+    return lib().krn_gemm_nn_workspace_for(a, b, m, n, k)
+
+
 def gemm_nn_call(in_dtype: Dtype, a: int, b: int, c: int, out_dtype: Dtype, m: int, n: int, k: int,
                  ops: list[tuple[int, float, int]], workspace: int, workspace_bytes: int):
-    """`gemm_nn` (B stored K x N, transposed into `workspace`) as a function of the stream, marshalled once."""
+    """`gemm_nn` (B stored K x N, read as it lies or transposed into `workspace`) as a function of the stream,
+    marshalled once."""
     count = len(ops)
     codes = (c_int * max(count, 1))(*(op for op, _, _ in ops))
     scalars = (c_float * max(count, 1))(*(s for _, s, _ in ops))

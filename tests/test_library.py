@@ -28,3 +28,23 @@ def test_the_library_loads_and_exports_every_declared_function():
     library = ctypes.CDLL(str(LIBRARY))
     missing = [name for name in declared() if not hasattr(library, name)]
     assert not missing, f"declared in include/krn_amd.h but not exported: {missing}"
+
+
+@pytest.mark.skipif(not LIBRARY.exists(), reason="libkrn_amd.so is not built (run __graft_entry__.build())")
+def test_nn_workspace_query_is_zero_exactly_for_the_products_read_as_they_lie():
+    """krn_gemm_nn_workspace_for is host arithmetic (no GPU call): 0 for the shapes the kernel reads B K x N as it
+    lies (N % 256 == 0, K % 64 == 0, K >= 128, at least 128 tiles of 256 x 256, 16-byte aligned operands),
+    otherwise the transposed operand's n * k * 2 bytes."""
+    library = ctypes.CDLL(str(LIBRARY))
+    query = library.krn_gemm_nn_workspace_for
+    query.restype = ctypes.c_int64
+    query.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    a, b = 1 << 20, 1 << 24  # aligned stand-in addresses: nothing is dereferenced
+    assert query(a, b, 8192, 8192, 8192) == 0
+    assert query(a, b, 2000, 4096, 192) == 0  # ragged M, an odd number of 128-byte slices
+    assert query(a, b, 8192, 8192 + 128, 8192) == (8192 + 128) * 8192 * 2  # N not a multiple of 256
+    assert query(a, b, 8192, 8192, 8192 + 32) == 8192 * (8192 + 32) * 2  # K not a multiple of 64
+    assert query(a, b, 8192, 8192, 64) == 8192 * 64 * 2  # a single slice
+    assert query(a, b, 1024, 4096, 4096) == 4096 * 4096 * 2  # 64 tiles: too few for the whole-tile loop
+    assert query(a + 8, b, 8192, 8192, 8192) == 8192 * 8192 * 2  # A not 16-byte aligned
+    assert query(a, b + 2, 8192, 8192, 8192) == 8192 * 8192 * 2  # B not 16-byte aligned
