@@ -226,8 +226,9 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--only", default="", help="comma list of extra legs to run (fa, fp8, int8, softmax, copy, "
-                        "blas); copy (the known-size calibration kernel for HBM byte counters) and blas (lib.matmul bf16 "
-                        "8192^3 through the hipBLASLt candidate and through ours) run only when named")
+                        "blas; default all but copy); copy (the known-size calibration kernel for HBM byte counters) "
+                        "runs only when named; blas is lib.matmul bf16 8192^3 NN through the hipBLASLt candidate and "
+                        "through ours")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the tile kernels shard by output "
@@ -241,7 +242,7 @@ def main() -> None:
     print("[bench] bf16 gemm 8192^3", file=sys.stderr, flush=True)
     ms, flops, (a, b, c) = gemm_bf16(device, args.steps, args.warmup, rng)
     tflops = flops / ms / 1e9
-    legs = set(filter(None, args.only.split(","))) or {"fa", "fp8", "int8", "softmax"}
+    legs = set(filter(None, args.only.split(","))) or {"fa", "fp8", "int8", "softmax", "blas"}
     extra = {}
     if "fa" in legs:
         print("[bench] causal bf16 flash attention", file=sys.stderr, flush=True)

@@ -1775,7 +1775,8 @@ __global__ __launch_bounds__(256) void transpose16(const uint16_t* __restrict__ 
 // panels addressable by 31-bit buffer offsets.
 static bool nn_direct(const void* a, const void* b, int64_t m, int64_t n, int64_t k) {
   const int64_t t256 = ((m + 255) / 256) * (n / 256);
-  return m > 0 && n > 0 && n % 256 == 0 && k % 64 == 0 && k >= 128 && t256 >= 128 && (uintptr_t)a % 16 == 0 &&
+  return m > 0 && n > 0 && n % 256 == 0 && k % 64 == 0 && k >= 128 && t256 >= 128 && t256 <= 0x7fffffff &&
+         (uintptr_t)a % 16 == 0 &&
          (uintptr_t)b % 16 == 0 && 256 * k * 2 <= 0x7fffffff && (k - 1) * n * 2 + 512 <= 0x7fffffff;
 }
 

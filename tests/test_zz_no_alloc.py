@@ -73,3 +73,27 @@ def test_no_alloc_nn_product_refuses_operands_beyond_its_scratch(device):
     code = library.lib().krn_gemm_nn_noalloc(library.kind(BF16), a.pointer, b.pointer, c.pointer, library.kind(BF16),
                                              16, n, k, 0, None, None, None, device.default_stream.handle)
     assert code != 0 and b"scratch" in library.lib().krn_amd_last_error()
+
+
+def test_no_alloc_nn_product_of_a_large_b_read_as_it_lies(device):
+    """A B of 69 MB, beyond the 64 MiB array: the kernel reads it K x N as it lies, so the no-alloc entry point takes
+    it (no scratch is used) and equals the NT product on B transposed on the host bit for bit; then a smaller call
+    through the array (the transposed path) right after it."""
+    rng = np.random.default_rng(79)
+    m, n, k = 2048, 8192, 4224
+    assert n * k * 2 > library.lib().krn_gemm_nn_noalloc_limit()
+    assert library.gemm_nn_workspace_for(1 << 20, 1 << 20, m, n, k) == 0
+    x, y = rng.standard_normal((m, k)).astype(np.float32), rng.standard_normal((k, n)).astype(np.float32)
+    aw, bw = bf16_words(x), bf16_words(y)
+    a, b = device.to_device(aw, T.bf16), device.to_device(bw, T.bf16)
+    bt = device.to_device(np.ascontiguousarray(bw.T), T.bf16)
+    want, got = device.empty(T.bf16, m, n), device.empty(T.bf16, m, n)
+    library.gemm_nt(BF16, a.pointer, bt.pointer, want.pointer, BF16, m, n, k, [], device.default_stream.handle)
+    no_alloc(device, BF16, a, b, got, m, n, k)
+    np.testing.assert_array_equal(got.to_host(), want.to_host())
+    m, n, k = 130, 200, 96
+    a, b, kind = operands(device, rng, BF16, m, n, k)
+    want, got = device.empty(kind, m, n), device.empty(kind, m, n)
+    with_workspace(device, BF16, a, b, want, m, n, k)
+    no_alloc(device, BF16, a, b, got, m, n, k)
+    np.testing.assert_array_equal(got.to_host(), want.to_host())
