@@ -1094,18 +1094,22 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
       }                                                                                                        \
     }                                                                                                          \
   } while (0)
+  // slice 0 through set 0 into stage 0; slices 1 .. NSET into the sets (set of slice j: j % NSET). With two sets,
+  // slice 1 is in flight while slice 0 lands.
   {
-    // slice 0 through set 0 into stage 0; slices 1 .. NSET into the sets (set of slice j: j % NSET)
     constexpr int SET_ = 0;
 #pragma unroll
     for (int q = 0; q < 16; ++q) KQ_LOAD(q, 0);
-#pragma unroll
-    for (int q = 0; q < 16; ++q) KQ_WRITE(q, 0);
   }
   if constexpr (NSET == 2) {
     constexpr int SET_ = 1;
 #pragma unroll
     for (int q = 0; q < 16; ++q) KQ_LOAD(q, min(1, nk - 1));
+  }
+  {
+    constexpr int SET_ = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) KQ_WRITE(q, 0);
   }
   {
     constexpr int SET_ = 0;
