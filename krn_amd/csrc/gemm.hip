@@ -2,11 +2,12 @@
 //
 // This is the lowering of krn's tile contraction `acc += a[rows, ks] @ b[cols, ks].transpose()` followed by
 // `c[rows, cols] = f(acc).to(dtype)` (reference compiler/ir.py:309-315 Accumulate, compiler/emit.py:788-821). One
-// workgroup owns a BM x BN output tile, four waves split it 2 x 2, and every wave keeps its accumulators in
-// registers as 32x32 MFMA blocks. Main loops: `gemm_quad` (bf16/f16/fp8), `gemm_pipe` (int8) and `gemm_pp` (fp8 with one slice) for
-// whole 256 x 256 tiles (see each; `gemm_pipe` also on 128 x 128 tiles for up to one wave of them),
-// `gemm_skinny` for M <= 128 (rings of direct-to-LDS slices per wave), and `gemm_tile` for the rest (128-byte
-// slices staged through registers, bounds-checked, double buffered). All end in the same epilogue, `patch_put` + `patch_store`.
+// workgroup owns a BM x BN output tile split among its waves, and every wave keeps its accumulators in registers as
+// 32x32 MFMA blocks. Main loops: `gemm_quad` (bf16/f16/fp8, also the NN form), `gemm_pipe` (int8) and `gemm_pp`
+// (fp8 with one slice) for whole 256 x 256 tiles (see each; `gemm_pipe` also on 128 x 128 and 128 x 256 tiles for
+// mid-size products), `gemm_skinny` for M <= 128 (rings of direct-to-LDS slices per wave), and `gemm_tile` for the
+// rest (128-byte slices staged through registers, bounds-checked, double buffered). All end in `store_tile`: whole
+// blocks straight from the accumulators (the direct epilogue), the rest through an LDS patch.
 //
 // One byte-oriented main loop serves three operand formats, because each MFMA consumes the same 16 bytes per lane
 // per half-wave:
@@ -901,17 +902,19 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
 
 // Four-wave main loop for whole 256 x 256 bf16/f16/fp8 tiles with K a multiple of 128 bytes. Each wave owns a 128 x 128
 // quarter (wave w: rows 128 (w >> 1), columns 128 (w & 1)), 16 accumulator blocks in AGPRs, one wave per SIMD.
-// 128-byte K slices go global -> registers -> LDS: slice kt + 2 is loaded into registers while slice kt multiplies,
-// and slice kt + 1 is written from those registers into the other of two LDS stages; the same 16 loads and 16 writes
-// per wave and slice as hipBLASLt's kernel makes. Every instruction of a slice has a fixed place (sched_barrier): per
+// 128-byte K slices go global -> registers -> LDS: while slice kt multiplies, slice kt + 1 is written from registers
+// into the other of two LDS stages and its registers are reloaded with slice kt + 3 (bf16/f16: two register sets,
+// so a slice has two slices of MFMA time to arrive; fp8, whose fragments take twice the registers: one set, slice
+// kt + 2); the same 16 loads and 16 writes per wave and slice as hipBLASLt's kernel makes. Every instruction of a slice has a fixed place (sched_barrier): per
 // MFMA step 16 MFMAs, each followed by at most one LDS read of the next step's fragments, one LDS write and one
 // global load, so the matrix core is never left waiting behind a burst of memory instructions; the one barrier per
 // slice comes after the eighth MFMA of the last step, once this wave's writes of slice kt + 1 have landed, and the
 // first fragments of slice kt + 1 are read in the shadow of the last eight MFMAs. Past the end the loads re-read the
 // last slice and the writes go to the stage that is not read again, so every slice runs the same code.
-// bf16 8192^3: 3-5 % faster than the eight-wave ring with direct-to-LDS slices, whose loads cost about a sixth of its
-// loop in LDS bandwidth (eight waves of 64 x 128 read 96 KiB of fragments per 64-byte slice, four of 128 x 128 read
-// 64 KiB per 128-byte slice).
+// bf16 8192^3: with one register set 3-5 % faster than the eight-wave ring with direct-to-LDS slices, whose loads
+// cost about a sixth of its loop in LDS bandwidth (eight waves of 64 x 128 read 96 KiB of fragments per 64-byte
+// slice, four of 128 x 128 read 64 KiB per 128-byte slice); the second set another 6 %. fp8 8192^3: 7 % faster than
+// the eight-wave ping-pong.
 //
 // NN: B is stored K x N (row k of B is `ldb` bytes apart, N a multiple of 256, 16-bit elements): a slice of B is 64
 // rows of 512 bytes kept in LDS as [k][n] with 16-byte chunk c of row k at slot c ^ 4 (k & 3), and every B fragment
