@@ -10,10 +10,10 @@ import numpy as np
 import pytest
 
 from krn_amd import T
-from krn_amd.dtypes import BF16, I8
+from krn_amd.dtypes import BF16, F16, I8
 from krn_amd.runtime import hipapi, library
 from oracle.numerics import bf16_values, bf16_words, e4m3_decode, e4m3_encode
-from tests.helpers import agree_bound
+from tests.helpers import agree_bound, assert_agrees
 from tests.kernels import tile_programs as programs
 
 pytestmark = pytest.mark.gpu
@@ -137,3 +137,45 @@ def test_direct_store_at_an_address_whose_low_word_has_bit_31_set(device, m, n, 
     got = np.empty((m, n), np.uint16)
     hipapi.api().hipMemcpy(got.ctypes.data, target, nbytes, hipapi.D2H)
     np.testing.assert_array_equal(got, want.to_host())
+
+
+# The four-wave whole-tile loop (at least 128 tiles of 256 x 256) runs its slices two at a time; these K give the
+# fewest slices it takes (2), an odd count (3, the tail slice) and 5, for bf16, f16 and fp8, with ragged M and N.
+@pytest.mark.parametrize("k_slices", [2, 3, 5])
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "fp8"])
+def test_four_wave_loop_at_its_slice_counts(device, dtype, k_slices):
+    m, n = 4096 - 40, 2048 + 256 * 4 - 24  # 16 x 12 = 192 tiles, the last row and column ragged
+    rng = np.random.default_rng(k_slices * 10 + len(dtype))
+    rows = np.r_[0:64, m - 64:m]  # the first and the last (ragged) row tiles, all columns
+    if dtype == "fp8":
+        k = 128 * k_slices
+        a = e4m3_encode(rng.standard_normal((m, k)).astype(np.float32))
+        b = e4m3_encode(rng.standard_normal((n, k)).astype(np.float32))
+        c = device.empty(T.bf16, m, n)
+        sa, sb = 0.5, 0.25
+        programs.gemm_fp8[programs.Tiling(bm=64, bn=64, bk=64)](
+            device.to_device(a, T.f8e4m3fn), device.to_device(b, T.f8e4m3fn), c, sa, sb)
+        got = bf16_values(c.to_host()[rows]).astype(np.float64)
+        da, db = e4m3_decode(a[rows]).astype(np.float64), e4m3_decode(b).astype(np.float64)
+        scale = np.float64(np.float32(sa * sb))
+        reference = (da @ db.T) * scale
+        bound = (8 * 2.0**-24 * (k + 8) * (np.abs(da) @ np.abs(db).T)) * scale + np.abs(reference) * 2.0**-8 * 1.01
+        assert np.all(np.abs(got - reference) <= bound + 1e-30)
+        return
+    k = 64 * k_slices
+    x, y = rng.standard_normal((m, k)).astype(np.float32), rng.standard_normal((n, k)).astype(np.float32)
+    if dtype == "bf16":
+        aw, bw, kind = bf16_words(x), bf16_words(y), T.bf16
+        av, bv = bf16_values(aw), bf16_values(bw)
+    else:
+        aw, bw, kind = x.astype(np.float16), y.astype(np.float16), T.f16
+        av, bv = aw.astype(np.float32), bw.astype(np.float32)
+    c = device.empty(kind, m, n)
+    if dtype == "bf16":  # krn's program
+        programs.gemm_nt[TILING](device.to_device(aw, kind), device.to_device(bw, kind), c)
+    else:  # the C ABI (no f16 NT program among the test programs)
+        da, db = device.to_device(aw, kind), device.to_device(bw, kind)
+        library.gemm_nt(F16, da.pointer, db.pointer, c.pointer, F16, m, n, k, [], device.default_stream.handle)
+    out = c.to_host()[rows]
+    got = bf16_values(out) if dtype == "bf16" else out.astype(np.float32)
+    assert_agrees(got, av[rows], bv.T, k, dtype)
