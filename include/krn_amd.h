@@ -74,10 +74,13 @@ int64_t krn_gemm_nn_workspace_for(const void* a, const void* b, int64_t m, int64
  * size). This entry point has no counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc,
  * hipFree or allocating library routine; it refuses a B whose n * k * 2 bytes exceed the limit when the product
- * needs the transposed copy (the products krn_gemm_nn reads B as it lies for use no scratch). The array is looked
- * up once per device (hipGetSymbolAddress) on that device's first call, with the stream's device current. Every call
- * on one GPU shares that GPU's array: calls that overlap on one GPU (concurrent streams, or another host thread)
- * race and must be ordered by the caller. */
+ * needs the transposed copy (the products krn_gemm_nn reads B as it lies for use no scratch). On a device's first
+ * call that uses the array, with the stream's device current, the library looks the array up (hipGetSymbolAddress)
+ * and creates one ordering event. The stream must belong to the current device (else an error). Every call on one
+ * GPU shares that GPU's array, and the library orders the calls that use it: each eager call makes its stream wait
+ * for the event recorded after the previous one, on any stream or host thread. A call on a stream under graph
+ * capture is not ordered that way: graph replays and eager calls that overlap on one GPU race, and the caller
+ * orders them. */
 int krn_gemm_nn_noalloc(int in_kind, const void* a, const void* b, void* c, int out_kind, int64_t m, int64_t n,
                         int64_t k, int nops, const int* ops, const float* scalars, const void* const* vectors,
                         void* stream);

@@ -1855,28 +1855,63 @@ extern "C" int krn_gemm_nn(int in_kind, const void* a, const void* b, void* c, i
 constexpr int64_t KRN_NN_SCRATCH_BYTES = (int64_t)64 << 20;
 static __device__ __align__(256) uint8_t scratch[KRN_NN_SCRATCH_BYTES];
 constexpr int KRN_MAX_DEVICES = 64;
-static std::mutex scratch_lock;
-static void* scratch_ptr[KRN_MAX_DEVICES] = {};
 
-// The device address of `scratch` on the calling thread's current device (looked up on that device's first call).
-static void* scratch_on_current_device() {
+// Per device: the array's address, and an event recorded after the last eager call that used it. Every call first
+// makes its stream wait (hipStreamWaitEvent, on the device) for that event, so two streams never hold the array at
+// once (on the previous call's own stream the wait is already satisfied by stream order; it is kept unconditional so
+// a stream handle reused after a destroy cannot skip it). The lock covers the look-up, that wait, the enqueue and the new record, so
+// host threads are ordered too. A stream under graph capture neither waits nor records (an event of the eager world
+// cannot order graph replays): a captured call is ordered only by the graph's and the caller's own dependencies.
+struct ScratchUse {
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;  // recorded after the last eager call that used the array
+  bool used = false;
+};
+static std::mutex scratch_lock;
+static ScratchUse scratch_use[KRN_MAX_DEVICES];
+
+// The device the call runs on: the stream's own device, which must be the current one (the address comes from
+// the current device's array). The null stream runs on the current device.
+static int scratch_device(hipStream_t stream) {
   int device = -1;
   hipError_t rc = hipGetDevice(&device);
   if (rc != hipSuccess || device < 0 || device >= KRN_MAX_DEVICES) {
     krn_set_error("gemm_nn_noalloc: no usable current device (%s, ordinal %d)", hipGetErrorString(rc), device);
-    return nullptr;
+    return -1;
   }
-  std::lock_guard<std::mutex> hold(scratch_lock);
-  if (scratch_ptr[device] == nullptr) {
-    void* ptr = nullptr;
-    rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (rc != hipSuccess || ptr == nullptr) {
-      krn_set_error("gemm_nn_noalloc: hipGetSymbolAddress of the scratch array failed: %s", hipGetErrorString(rc));
-      return nullptr;
+  if (stream != nullptr) {
+    int of_stream = -1;
+    rc = hipStreamGetDevice(stream, &of_stream);
+    if (rc != hipSuccess) {
+      krn_set_error("gemm_nn_noalloc: hipStreamGetDevice failed: %s", hipGetErrorString(rc));
+      return -1;
     }
-    scratch_ptr[device] = ptr;
+    if (of_stream != device) {
+      krn_set_error("gemm_nn_noalloc: the stream belongs to device %d but device %d is current; make the stream's "
+                    "device current", of_stream, device);
+      return -1;
+    }
   }
-  return scratch_ptr[device];
+  return device;
+}
+
+// Set-up of one device, on its first call, with the lock held: the array's address and the ordering event.
+static bool scratch_setup(int device) {
+  ScratchUse& use = scratch_use[device];
+  if (use.ptr != nullptr) return true;
+  void* ptr = nullptr;
+  hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (rc != hipSuccess || ptr == nullptr) {
+    krn_set_error("gemm_nn_noalloc: hipGetSymbolAddress of the scratch array failed: %s", hipGetErrorString(rc));
+    return false;
+  }
+  rc = hipEventCreateWithFlags(&use.done, hipEventDisableTiming);
+  if (rc != hipSuccess) {
+    krn_set_error("gemm_nn_noalloc: hipEventCreateWithFlags failed: %s", hipGetErrorString(rc));
+    return false;
+  }
+  use.ptr = ptr;
+  return true;
 }
 
 extern "C" int64_t krn_gemm_nn_noalloc_limit(void) { return KRN_NN_SCRATCH_BYTES; }
@@ -1891,9 +1926,33 @@ extern "C" int krn_gemm_nn_noalloc(int in_kind, const void* a, const void* b, vo
                   (long long)KRN_NN_SCRATCH_BYTES);
     return -1;
   }
-  void* bt = nullptr;
-  if (need > 0 && (bt = scratch_on_current_device()) == nullptr) return -1;
-  return gemm_nn_through(in_kind, a, b, c, out_kind, m, n, k, nops, ops, scalars, vectors, bt, stream);
+  if (need == 0) return gemm_nn_through(in_kind, a, b, c, out_kind, m, n, k, nops, ops, scalars, vectors, nullptr,
+                                        stream);
+  hipStream_t s = (hipStream_t)stream;
+  const int device = scratch_device(s);
+  if (device < 0) return -1;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  hipError_t rc = hipStreamIsCapturing(s, &capture);
+  if (rc != hipSuccess) {
+    krn_set_error("gemm_nn_noalloc: hipStreamIsCapturing failed: %s", hipGetErrorString(rc));
+    return -1;
+  }
+  const bool eager = capture == hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> hold(scratch_lock);
+  if (!scratch_setup(device)) return -1;
+  ScratchUse& use = scratch_use[device];
+  if (eager && use.used && (rc = hipStreamWaitEvent(s, use.done, 0)) != hipSuccess) {
+    krn_set_error("gemm_nn_noalloc: hipStreamWaitEvent failed: %s", hipGetErrorString(rc));
+    return -1;
+  }
+  const int status = gemm_nn_through(in_kind, a, b, c, out_kind, m, n, k, nops, ops, scalars, vectors, use.ptr, s);
+  if (status != 0 || !eager) return status;
+  if ((rc = hipEventRecord(use.done, s)) != hipSuccess) {
+    krn_set_error("gemm_nn_noalloc: hipEventRecord failed: %s", hipGetErrorString(rc));
+    return -1;
+  }
+  use.used = true;
+  return 0;
 }
 
 // Whole 128 x 128 tiles (rows and cols multiples of 128, 16-byte aligned): rows land in LDS with 16-byte loads (256

@@ -6,6 +6,7 @@ Host storage follows krn: bf16 tensors are raw `uint16` words and fp8 tensors ar
 type says the format (reference README; tests/compiler/test_tensor_cores.py:305-311).
 """
 
+import typing
 from dataclasses import dataclass
 from enum import Enum
 
@@ -111,11 +112,35 @@ def common(a: Dtype, b: Dtype) -> Dtype | None:
     return None
 
 
+# krn's element types are parametrised classes (reference src/krn/frontend/numerics.py:343-384): `fp[E, M, kind]`
+# with literal exponent and mantissa widths, `sint[N]` and `uint[N]`. (family, parameters) -> the type they name.
+_STRUCTURAL = {
+    ("fp", (11, 52, "ieee")): F64, ("fp", (8, 23, "ieee")): F32, ("fp", (5, 10, "ieee")): F16,
+    ("fp", (8, 7, "ieee")): BF16, ("fp", (4, 3, "fn")): F8E4M3, ("fp", (5, 2, "ieee")): F8E5M2,
+    ("sint", (8,)): I8, ("sint", (16,)): I16, ("sint", (32,)): I32, ("sint", (64,)): I64,
+    ("uint", (8,)): U8, ("uint", (16,)): U16, ("uint", (32,)): U32, ("uint", (64,)): U64,
+}  # fmt: skip
+
+
+def _parameter(arg: object) -> object:
+    """A literal width (`L[8]` -> 8) or a format kind class (`ieee` -> "ieee")."""
+    literal = typing.get_args(arg)
+    if typing.get_origin(arg) is typing.Literal and len(literal) == 1:
+        return literal[0]
+    return getattr(arg, "__name__", arg)
+
+
 def of(value: object) -> Dtype:
-    """The element type named by a kernel annotation object or a frontend dtype class."""
+    """The element type named by a kernel annotation object, a frontend dtype class of this package, or one of
+    krn's own parametrised element types (`fp[L[8], L[7], ieee]` is bf16)."""
     if isinstance(value, Dtype):
         return value
     name = getattr(value, "dtype_name", None) or getattr(value, "__name__", None)
     if name in BY_NAME:
         return BY_NAME[name]
+    origin = typing.get_origin(value)
+    if origin is not None:
+        key = (getattr(origin, "__name__", None), tuple(_parameter(a) for a in typing.get_args(value)))
+        if key in _STRUCTURAL:
+            return _STRUCTURAL[key]
     raise TypeError(f"{value!r} is not an element type")

@@ -88,7 +88,10 @@ class _ConstAlias:
 
 
 def is_const(annotation: object) -> bool:
-    return isinstance(annotation, _ConstAlias) or get_origin(annotation) is Const or (
+    """Whether a field annotation is `Const[...]`: this module's, or krn's own (`type Const[T] = T`, reference
+    src/krn/frontend/records.py:17, whose subscript has that alias as its origin), or the same written as a string."""
+    origin = get_origin(annotation)
+    return isinstance(annotation, _ConstAlias) or origin is Const or getattr(origin, "__name__", None) == "Const" or (
         isinstance(annotation, str) and annotation.startswith("Const[")
     )
 

@@ -19,12 +19,18 @@ from krn_amd.dtypes import BF16, F16, F32, Dtype
 from krn_amd.runtime.api import Stream, current_stream, default_device
 
 
-class Op(Enum):
+class Op(str, Enum):
+    """Library operations. A `str` enum, as the reference's StrEnum (lib.py:76-79): `Op.MATMUL == "matmul"`."""
+
     MATMUL = "matmul"
 
+    def __str__(self) -> str:
+        return self.value
 
-class Epilogue(Enum):
-    """What follows the product, in the reference's names (lib.py `Epilogue`)."""
+
+class Epilogue(str, Enum):
+    """What follows the product, in the reference's names (lib.py:82-91 `Epilogue`, a StrEnum): members compare
+    equal to their string values, and `matmul(..., epilogue="bias_gelu")` is accepted."""
 
     NONE = "none"
     BIAS = "bias"
@@ -33,6 +39,9 @@ class Epilogue(Enum):
     BIAS_RELU = "bias_relu"
     BIAS_GELU = "bias_gelu"
     SILU = "silu"
+
+    def __str__(self) -> str:
+        return self.value
 
     @property
     def has_bias(self) -> bool:
@@ -136,15 +145,20 @@ FLOATS = (F16, BF16, F32)
 def matmul(a, b, *, epilogue: Epilogue = Epilogue.NONE, bias=None, out=None, library: str | None = None):
     """`a @ b` with an optional fused epilogue, enqueued on the current stream; returns `out`, allocated when not
     given (reference lib.py:581-615). `library` names one candidate instead of the preference order."""
+    epilogue = Epilogue(epilogue)
     if len(a.shape) != 2 or len(b.shape) != 2 or a.shape[1] != b.shape[0]:
         raise ValueError(f"matmul needs (m, k) @ (k, n) matrices, got {a.shape} @ {b.shape}")
     if epilogue.has_bias and (bias is None or tuple(bias.shape) != (b.shape[1],)):
         raise ValueError(f"{epilogue.value} needs a bias vector of length {b.shape[1]}")
+    result_type = out.dtype if out is not None else product_type(a.dtype, b.dtype)
+    if epilogue.has_bias and bias.dtype != result_type:
+        # the bias is a vector of the output type (reference lib.py:576-590 `Vector[Y]`); every candidate reads it so
+        raise ValueError(f"{epilogue.value} needs a {result_type} bias (the output type), got {bias.dtype}")
     device = default_device()
     stream = current_stream.get() or device.default_stream
-    result = out if out is not None else device.empty(product_type(a.dtype, b.dtype), a.shape[0], b.shape[1])
-    if tuple(result.shape) != (a.shape[0], b.shape[1]):
-        raise ValueError(f"out has shape {result.shape}, the product {(a.shape[0], b.shape[1])}")
+    if out is not None and tuple(out.shape) != (a.shape[0], b.shape[1]):
+        raise ValueError(f"out has shape {out.shape}, the product {(a.shape[0], b.shape[1])}")
+    result = out if out is not None else device.empty(result_type, a.shape[0], b.shape[1])
     problem = Problem(Op.MATMUL, (a.dtype, b.dtype, result.dtype), (a.shape[0], b.shape[1], a.shape[1]), epilogue)
     launch(problem, Operands(a, b, result, bias), stream, library)
     return result

@@ -191,6 +191,18 @@ def _destroy(owned: list[tuple[str, int]]) -> None:
     owned.clear()
 
 
+def alignment(pointer: int) -> int:
+    """The largest power of two up to 256 that divides a device address."""
+    return min(256, pointer & -pointer) if pointer else 256
+
+
+def alignments(operands: Operands | None) -> tuple[int, ...]:
+    if operands is None:
+        return ()
+    return tuple(alignment(t.pointer) if t is not None else 0
+                 for t in (operands.a, operands.b, operands.out, operands.bias))
+
+
 class Session(threading.local):
     """One hipBLASLt handle and plan cache per thread."""
 
@@ -198,13 +210,18 @@ class Session(threading.local):
         self.handle: int | None = None
         self.plans: dict[tuple, Plan] = {}
 
-    def plan(self, problem: Problem) -> Plan:
+    def plan(self, problem: Problem, operands: Operands | None = None) -> Plan:
+        """The plan of `problem` for operands of these pointer alignments. As the reference's cuBLASLt adapter keys
+        its plans (lib_cublaslt.py:110-135 `PlanKey.alignments`), an algorithm chosen for aligned operands is never
+        replayed on less aligned ones. hipBLASLt's preference attributes have no minimum-alignment entries (only
+        search mode and workspace size, hipblaslt.h `hipblasLtMatmulPreferenceAttributes_t`), so the key is what
+        carries the alignment."""
         if self.handle is None:
             handle = c_void_p()
             api()("hipblasLtCreate", byref(handle))
             self.handle = handle.value
             weakref.finalize(self, api().raw, "hipblasLtDestroy", c_void_p(handle.value))
-        key = (problem.dtypes, problem.shape, problem.epilogue)
+        key = (problem.dtypes, problem.shape, problem.epilogue, alignments(operands))
         if key not in self.plans:
             self.plans[key] = Plan(self.handle, problem)
         return self.plans[key]
@@ -227,7 +244,7 @@ class HipblasLt(Candidate):
         return refusal(problem)
 
     def run(self, problem: Problem, operands: Operands, stream: Stream) -> None:
-        plan = _session.plan(problem)
+        plan = _session.plan(problem, operands)
         plan.enqueue(_session.handle, operands, stream)
         stream.note("lib.matmul hipblaslt", (operands.a, operands.b, operands.out, operands.bias))
 

@@ -455,6 +455,20 @@ def _scalar_value(e: ir.Expr, params: dict) -> np.float32:
     raise ValueError(f"{type(e).__name__} is not a scalar epilogue operand")
 
 
+def _blocks(launch: object) -> Blocks | None:
+    """An explicit grid from any geometry object with the reference's public fields (src/krn/frontend/geometry.py:
+    8-43): `Tiles` (`shape`, `tile`, `.blocks`) or `Blocks` (`x`, `y`, `z`, `threads`). `Items` launches one thread
+    per item, which a tile program does not: it is refused."""
+    if launch is None or isinstance(launch, Blocks):
+        return launch
+    if hasattr(launch, "blocks"):
+        launch = launch.blocks
+    if all(hasattr(launch, axis) for axis in ("x", "y", "z")):
+        return Blocks(int(launch.x), int(launch.y), int(launch.z), getattr(launch, "threads", None))
+    raise TargetError(f"{type(launch).__name__} geometry", TARGET, "it is not a tile launch geometry (one thread per "
+                      "item is not how a tile program runs)", "launch with Blocks or Tiles")
+
+
 _plans: dict[tuple, Launch] = {}  # (kernel, argument kinds) -> its captured IR and plan
 _plans_lock = threading.Lock()
 
@@ -462,9 +476,11 @@ _plans_lock = threading.Lock()
 class HIPLauncher(Launcher):
     """A kernel with an optional explicit geometry. The first call of a signature captures and plans it."""
 
-    def __init__(self, device: "HIPDevice", kernel: Kernel, launch: Blocks | None) -> None:
-        self.device, self.kernel, self.launch = device, kernel, launch
-        self.parameters = kernel.parameters
+    def __init__(self, device: "HIPDevice", kernel: Kernel, launch: object = None) -> None:
+        # only `fn` and `name` are read, as the reference's SourceLauncher does (src/krn/runtime/runtime.py:463-470),
+        # so krn's own Kernel objects launch here unchanged
+        self.device, self.kernel, self.launch = device, kernel, _blocks(launch)
+        self.parameters = tuple(inspect.signature(kernel.fn).parameters)
 
     def ordered(self, args: tuple, kwargs: dict) -> tuple:
         if not kwargs and len(args) == len(self.parameters):

@@ -80,3 +80,49 @@ def test_the_generic_matmul_program_takes_its_element_type_from_the_arguments(dt
 def test_a_generic_tensor_needs_its_argument():
     with pytest.raises(CaptureError, match="generic over F"):
         capture(kernels.__file__, "matmul_epilogue", consts={"t": {"bm": 16, "bn": 16, "bk": 8}})
+
+
+def test_a_bias_of_another_type_than_the_output_is_refused_before_anything_runs(monkeypatch):
+    """The bias is a vector of the output type (reference lib.py:576-590 `bias: Vector[Y]`, `out: Matrix[Y]`).
+    hipBLASLt reads it as the output type, so a mismatch is refused before any device call."""
+    from types import SimpleNamespace
+
+    def touched(*args, **kwargs):
+        raise AssertionError("nothing may be allocated or launched")
+
+    monkeypatch.setattr(lib, "default_device", touched)
+    monkeypatch.setattr(lib, "launch", touched)
+    a, b = SimpleNamespace(shape=(4, 6), dtype=BF16), SimpleNamespace(shape=(6, 5), dtype=BF16)
+    out = SimpleNamespace(shape=(4, 5), dtype=F32)
+    with pytest.raises(ValueError, match="needs a f32 bias"):
+        lib.matmul(a, b, epilogue=lib.Epilogue.BIAS, bias=SimpleNamespace(shape=(5,), dtype=BF16), out=out)
+    with pytest.raises(ValueError, match="needs a bf16 bias"):
+        lib.matmul(a, b, epilogue="bias_gelu", bias=SimpleNamespace(shape=(5,), dtype=F32))
+
+
+def test_epilogues_and_ops_compare_equal_to_their_names():
+    """The reference's Epilogue and Op are StrEnums (lib.py:76-91)."""
+    assert lib.Epilogue.BIAS_GELU == "bias_gelu" and lib.Epilogue("silu") is lib.Epilogue.SILU
+    assert str(lib.Epilogue.RELU) == "relu" and lib.Op.MATMUL == "matmul"
+
+
+def test_hipblaslt_plans_are_keyed_on_operand_alignment(monkeypatch):
+    """An algorithm chosen for 256-byte aligned operands is not replayed on less aligned ones (reference
+    lib_cublaslt.py:110-135 `PlanKey.alignments`)."""
+    from types import SimpleNamespace
+
+    from krn_amd.lib import lib_hipblaslt as lt
+
+    made = []
+    monkeypatch.setattr(lt, "Plan", lambda handle, problem: made.append(problem) or SimpleNamespace())
+    session = lt.Session()
+    session.handle = 1
+    p = problem((BF16,) * 3)
+    t = lambda pointer: SimpleNamespace(pointer=pointer)
+    aligned = lib.Operands(t(0x10000), t(0x20000), t(0x30000), None)
+    session.plan(p, aligned)
+    session.plan(p, lib.Operands(t(0x40000), t(0x50100), t(0x60000), None))
+    assert len(made) == 1  # 0x50100 is still 256-byte aligned
+    session.plan(p, lib.Operands(t(0x40000), t(0x50002), t(0x60000), None))
+    assert len(made) == 2
+    assert lt.alignments(lib.Operands(t(0x50002), t(0x50040), t(0x1000), None)) == (2, 64, 256, 0)

@@ -1,7 +1,8 @@
 """krn_gemm_nn_noalloc, the NN product for callers that cannot allocate (code under graph capture, serving loops,
 harnesses that forbid hipMalloc): the transposed operand lives in the library's own device array instead of a
 workspace. Called through the C ABI and checked bit for bit against krn_gemm_nn with a workspace, on two calls in a
-row, the second smaller, and refused beyond its limit."""
+row, the second smaller, and refused beyond its limit; it allocates nothing across calls, is ordered between two
+streams that share the array, and replays correctly from a captured graph."""
 
 import numpy as np
 import pytest
@@ -31,11 +32,15 @@ def with_workspace(device, dtype, a, b, c, m, n, k, ops=(), vectors=()):
     device.default_stream.sync()
 
 
-def no_alloc(device, dtype, a, b, c, m, n, k, ops=(), vectors=()):
+def enqueue_no_alloc(dtype, a, b, c, m, n, k, stream_handle, ops=(), vectors=()):
     codes, scalars, vecs = library.marshal_ops([(op, 0.0, v) for op, v in zip(ops, vectors)])
     library.check(library.lib().krn_gemm_nn_noalloc(library.kind(dtype), a.pointer, b.pointer, c.pointer,
                                                     library.kind(dtype), m, n, k, len(ops), codes, scalars, vecs,
-                                                    device.default_stream.handle), "krn_gemm_nn_noalloc")
+                                                    stream_handle), "krn_gemm_nn_noalloc")
+
+
+def no_alloc(device, dtype, a, b, c, m, n, k, ops=(), vectors=()):
+    enqueue_no_alloc(dtype, a, b, c, m, n, k, device.default_stream.handle, ops, vectors)
     device.default_stream.sync()
 
 
@@ -97,3 +102,82 @@ def test_no_alloc_nn_product_of_a_large_b_read_as_it_lies(device):
     with_workspace(device, BF16, a, b, want, m, n, k)
     no_alloc(device, BF16, a, b, got, m, n, k)
     np.testing.assert_array_equal(got.to_host(), want.to_host())
+
+
+def test_no_alloc_calls_allocate_no_device_memory(device):
+    """After a first call (the per-device set-up), further transposing calls leave the free device memory as it was."""
+    from krn_amd.runtime import hipapi
+
+    rng = np.random.default_rng(80)
+    m, n, k = 384, 640, 768
+    a, b, kind = operands(device, rng, BF16, m, n, k)
+    want, got = device.empty(kind, m, n), device.empty(kind, m, n)
+    with_workspace(device, BF16, a, b, want, m, n, k)
+    no_alloc(device, BF16, a, b, got, m, n, k)
+    device.sync()
+    before = hipapi.memory_free()
+    for _ in range(5):
+        no_alloc(device, BF16, a, b, got, m, n, k)
+    device.sync()
+    assert hipapi.memory_free() == before
+    np.testing.assert_array_equal(got.to_host(), want.to_host())
+
+
+def test_no_alloc_calls_on_two_streams_are_ordered(device):
+    """Two streams alternate transposing calls with different B operands, enqueued back to back with no host wait:
+    the library makes each call wait for the previous user of the shared array, so every result is right."""
+    rng = np.random.default_rng(81)
+    first, second = device.stream(), device.stream()
+    cases = []
+    for m, n, k in [(4096, 2048, 4096), (256, 1920, 4096), (2048, 2048, 2048), (128, 384, 256)]:
+        a, b, kind = operands(device, rng, F16, m, n, k)
+        want, got = device.empty(kind, m, n), device.empty(kind, m, n)
+        with_workspace(device, F16, a, b, want, m, n, k)
+        cases.append((a, b, want, got, m, n, k))
+    device.sync()
+    for repeat in range(2):
+        for i, (a, b, _, got, m, n, k) in enumerate(cases):
+            enqueue_no_alloc(F16, a, b, got, m, n, k, (first if i % 2 == 0 else second).handle)
+        first.sync()
+        second.sync()
+        for a, b, want, got, m, n, k in cases:
+            np.testing.assert_array_equal(got.to_host(), want.to_host(), err_msg=f"{m}x{n}x{k} pass {repeat}")
+
+
+def test_no_alloc_call_takes_a_stream_of_the_current_device(device):
+    """The array's address is the current device's: a stream's own device must be the current one. With one GPU
+    every stream matches: a created stream (not the default one) is accepted and its call is right."""
+    rng = np.random.default_rng(82)
+    m, n, k = 64, 128, 64
+    a, b, kind = operands(device, rng, BF16, m, n, k)
+    want, got = device.empty(kind, m, n), device.empty(kind, m, n)
+    with_workspace(device, BF16, a, b, want, m, n, k)
+    other = device.stream()
+    enqueue_no_alloc(BF16, a, b, got, m, n, k, other.handle)
+    other.sync()
+    np.testing.assert_array_equal(got.to_host(), want.to_host())
+
+
+def test_no_alloc_call_replays_from_a_captured_graph(device):
+    """One transposing call recorded into a hipGraph (the caller the entry point is for) and replayed three times,
+    with eager no-alloc calls on other operands and a synchronization between replays: every replay equals the
+    workspace entry point."""
+    rng = np.random.default_rng(83)
+    m, n, k = 320, 768, 512
+    a, b, kind = operands(device, rng, BF16, m, n, k)
+    want, got = device.empty(kind, m, n), device.empty(kind, m, n)
+    with_workspace(device, BF16, a, b, want, m, n, k)
+    x, y, _ = operands(device, rng, BF16, 192, 640, 256)
+    other_want, other_got = device.empty(kind, 192, 640), device.empty(kind, 192, 640)
+    with_workspace(device, BF16, x, y, other_want, 192, 640, 256)
+    device.sync()
+    graph = device.graph(lambda: enqueue_no_alloc(BF16, a, b, got, m, n, k, device.launch_stream().handle))
+    zero = np.zeros((m, n), np.uint16)
+    for replay in range(3):
+        got.copy_from(zero)
+        device.sync()
+        graph()
+        device.sync()
+        np.testing.assert_array_equal(got.to_host(), want.to_host(), err_msg=f"replay {replay}")
+        no_alloc(device, BF16, x, y, other_got, 192, 640, 256)
+        np.testing.assert_array_equal(other_got.to_host(), other_want.to_host(), err_msg=f"eager after {replay}")
