@@ -22,6 +22,7 @@ f16/bf16 MFMA only, refused fp8 (compiler/matrix.py:129-139) and had no int8 pro
 """
 
 import dataclasses
+import math
 from dataclasses import dataclass, field
 
 from krn_amd.compiler import ir
@@ -63,11 +64,13 @@ class AttentionPlan:
     k: str
     v: str
     o: str
-    scale: str
+    scale: tuple  # the dataflow of the scalar the scores are multiplied by (dataflow.scalar_value evaluates it)
     dtype: Dtype
     d: int
     bq: int
     causal: bool
+    base: float = 1.0  # the exponent's base as a power of 2: 1 for exp2, log2(e) for exp
+    rank: int = 3  # 3: (heads, seq, d); 4: (batch, heads, seq, d)
 
 
 @dataclass(frozen=True)
@@ -249,30 +252,144 @@ def _scalar_expr(e: ir.Expr) -> bool:
     return False
 
 
+def _strip_cast(x: tuple) -> tuple:
+    return x[2] if x[0] == "cast" else x
+
+
+def _const(x: tuple, value: float) -> bool:
+    return x[0] == "const" and x[1] == value
+
+
+def _masked_value(x: tuple) -> bool:
+    """A constant at or below -1e30 (or -inf): exp2 of it minus any finite row maximum is 0."""
+    return x[0] in ("const", "fill") and not isinstance(x[1], bool) and x[1] <= -1.0e30
+
+
 def match_attention(kernel: ir.Kernel) -> AttentionPlan | None:
-    """krn's flash-attention program, recognised by comparing the IR with the canonical program's IR, captured
-    with the same configuration and element types, after renaming every variable and parameter positionally."""
-    from krn_amd.compiler import programs
+    """krn's flash-attention program (reference examples/04_libraries/08_flash_attention.py:35-59), recognised by
+    what it computes: one loop over key tiles `c` of a key or value tensor's sequence axis, carrying a running row
+    maximum `m`, row sum `l` and output `acc` started at (<= -1e30, 0, 0), with one iteration
+
+        s = scale * (Q @ K[c:c+bk].T)             (scale: a scalar expression; optionally masked to <= -1e30 where
+                                                   k_pos > q_pos, k_pos = c + arange(bk), q_pos = rows + arange(bq))
+        m' = maximum(m, rowmax(s)),  p = exp2(s - m'),  corr = exp2(m - m')
+        l' = l * corr + rowsum(p),   acc' = acc * corr + p.to(dtype) @ V[c:c+bk]
+
+    (or exp in place of both exp2, which is exp2 with the scale times log2(e)), and one store `o[rows] = (acc /
+    l).to(dtype)`; Q, K, V and O are (heads, seq, d) tensors indexed by block y, or (batch, heads, seq, d) indexed
+    by blocks z and y, with the query rows `block.tile(bq)` along x. Names, temporaries, statement order, operand
+    order of commutative operations and the tiling (bq, bk) are free. The dataflow is compared, not the spelling."""
+    from krn_amd.compiler import dataflow as df
 
     tensors = [(n, t) for n, t in kernel.params if isinstance(t, ir.TensorType)]
-    scalars = [(n, t) for n, t in kernel.params if not isinstance(t, ir.TensorType)]
-    if len(tensors) != 4 or len(scalars) != 1 or any(t.rank != 3 for _, t in tensors):
+    if len(tensors) != 4 or len({t.rank for _, t in tensors}) != 1 or tensors[0][1].rank not in (3, 4):
         return None
+    rank = tensors[0][1].rank
     dtype = tensors[0][1].dtype
-    if dtype not in (F16, BF16) or any(t.dtype != dtype for _, t in tensors) or scalars[0][1] != F32:
+    if dtype not in (F16, BF16) or any(t.dtype != dtype for _, t in tensors):
         return None
-    consts = dict(kernel.consts)
-    if len(consts) != 1:
+    try:
+        flow = df.evaluate(kernel)
+    except (df.Unsupported, KeyError, IndexError, TypeError):
         return None
-    values = dict(next(iter(consts.values())))
-    if set(values) != {"bq", "bk", "d", "causal"} or values["d"] not in (64, 128):
+    if len(flow.loops) != 1 or len(flow.stores) != 1:
         return None
-    canonical = programs.attention(values, dtype)
-    if programs.canonical_form(kernel) != programs.canonical_form(canonical):
+    loop, (o_name, o_slices, stored) = flow.loops[0], flow.stores[0]
+    heads = (((("block", "y"), 1, True),) if rank == 3 else ((("block", "z"), 1, True), (("block", "y"), 1, True)))
+    # the store: o[heads, rows, 0:d] = (acc / l).to(dtype)
+    if not (stored[0] == "cast" and stored[1] == dtype and stored[2][0] == "bin" and stored[2][1] == "/"):
         return None
-    names = [n for n, _ in kernel.params]
-    return AttentionPlan(names[0], names[1], names[2], names[3], names[4], dtype, int(values["d"]),
-                         int(values["bq"]), bool(values["causal"]))
+    acc_f, l_f = stored[2][2], stored[2][3]
+    if acc_f[0] != "final" or l_f[0] != "final":
+        return None
+    acc, l = acc_f[1], l_f[1]
+    if len(o_slices) != rank or o_slices[:-2] != heads:
+        return None
+    rows, d_slice = o_slices[-2], o_slices[-1]
+    bq, d = rows[1], d_slice[1]
+    if rows[2] or rows[0] != ("bin", "*", *sorted((("block", "x"), ("const", float(bq))), key=repr)):
+        return None
+    if d_slice != (("const", 0.0), d, False) or d not in (64, 128):
+        return None
+    carried = set(loop.init)
+    if not {acc, l} <= carried or len(carried) != 3:
+        return None
+    (m,) = carried - {acc, l}
+    # initial values
+    if loop.init[acc] != ("fill", 0.0, (bq, d)) or loop.init[l] != ("fill", 0.0, (bq, 1)):
+        return None
+    if not (_masked_value(loop.init[m]) and (loop.init[m][0] == "const" or loop.init[m][2] == (bq, 1))):
+        return None
+    # m' = maximum(m, rowmax(s))
+    m_new = loop.update[m]
+    if not (m_new[0] == "math" and m_new[1] == "maximum" and ("state", m) in m_new[2:]):
+        return None
+    rowmax = m_new[3] if m_new[2] == ("state", m) else m_new[2]
+    if not (rowmax[0] == "reduce" and rowmax[1:4] == ("max", 1, True)):
+        return None
+    s = rowmax[4]
+    # l' = l * corr + rowsum(p);  acc' = acc * corr + p.to(dtype) @ V
+    def split(update: tuple, state: str) -> tuple[tuple, tuple] | None:
+        if not (update[0] == "bin" and update[1] == "+"):
+            return None
+        for scaled, other in ((update[2], update[3]), (update[3], update[2])):
+            if scaled[0] == "bin" and scaled[1] == "*" and ("state", state) in scaled[2:]:
+                corr = scaled[3] if scaled[2] == ("state", state) else scaled[2]
+                return corr, other
+        return None
+    l_parts, acc_parts = split(loop.update[l], l), split(loop.update[acc], acc)
+    if l_parts is None or acc_parts is None or l_parts[0] != acc_parts[0]:
+        return None
+    corr, rowsum = l_parts
+    fn = corr[1] if corr[0] == "math" else None
+    if fn not in ("exp2", "exp") or corr[2] != ("bin", "-", ("state", m), m_new):
+        return None
+    p = ("math", fn, ("bin", "-", s, m_new))
+    if rowsum != ("reduce", "sum", 1, True, p):
+        return None
+    pv = acc_parts[1]
+    if not (pv[0] == "matmul" and pv[1] == ("cast", dtype, p) and pv[2][0] == "load"):
+        return None
+    v_load = pv[2]
+    # s = scale * (Q @ K.T), optionally masked
+    causal = False
+    if s[0] == "select":
+        cond, s0, masked = s[1], s[2], s[3]
+        if not _masked_value(masked):
+            return None
+        # k_pos <= q_pos: arange along keys from the loop variable, along rows from the rows' start
+        if not (cond[0] == "bin" and cond[1] == "<="):
+            return None
+        k_pos, q_pos = cond[2], cond[3]
+        if not (k_pos[0] == "arange" and k_pos[1] == 1 and _strip_cast(k_pos[3]) == ("loopvar", loop.var)):
+            return None
+        if not (q_pos[0] == "arange" and q_pos[1] == 0 and q_pos[2] == (bq, 1) and _strip_cast(q_pos[3]) == rows[0]):
+            return None
+        causal = True
+        s = s0
+    if not (s[0] == "bin" and s[1] == "*"):
+        return None
+    product = next((x for x in s[2:] if x[0] == "matmul"), None)
+    scale = s[2] if s[3] is product else s[3]
+    if product is None or not df.is_scalar(scale):
+        return None
+    q_load, kt = product[1], product[2]
+    if not (q_load[0] == "load" and kt[0] == "transpose" and kt[1][0] == "load"):
+        return None
+    k_load = kt[1]
+    if q_load[2] != (*heads, rows, d_slice):
+        return None
+    bk = k_load[2][-2][1]
+    if bk != loop.step or not _const(loop.lo, 0.0):
+        return None
+    key_slices = (*heads, (("loopvar", loop.var), bk, False), d_slice)
+    if k_load[2] != key_slices or v_load[2] != key_slices:
+        return None
+    names = {q_load[1], k_load[1], v_load[1], o_name}
+    if len(names) != 4 or loop.hi not in (("dim", k_load[1], rank - 2), ("dim", v_load[1], rank - 2)):
+        return None
+    return AttentionPlan(q_load[1], k_load[1], v_load[1], o_name, scale, dtype, int(d), int(bq), causal,
+                         1.0 if fn == "exp2" else math.log2(math.e), rank)
 
 
 def match_softmax(kernel: ir.Kernel) -> SoftmaxPlan | None:
@@ -314,8 +431,8 @@ def why_generic(kernel: ir.Kernel) -> list[str]:
                        ".transpose()` (or `b[ks, cols]`) of bf16/f16/fp8/int8 operands, one store of an epilogue of "
                        "scalar or row/column vector mul/add and relu/gelu/silu")
     if match_attention(kernel) is None:
-        reasons.append("not krn's flash-attention program with head dimension 64 or 128 and f16/bf16 (compared with "
-                       "the canonical program's IR)")
+        reasons.append("not krn's flash-attention program (its dataflow: an online softmax over key tiles with "
+                       "exp2 or exp, an optional causal mask, head dimension 64 or 128, f16/bf16 tensors)")
     if match_softmax(kernel) is None:
         reasons.append("not one of krn's row-softmax programs (compared with the canonical programs' IR)")
     return reasons

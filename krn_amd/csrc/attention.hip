@@ -20,8 +20,9 @@
 // transposing copy (chunk c of key row r at slot c ^ 4 (r & 3)). The key loop is software-pipelined in 32-key
 // halves: the score MFMAs of half h + 1 are issued before the exp2 / sum / pack of half h, so the matrix core and
 // the vector ALU of one wave work at the same time. Each SIMD interleaves two waves of the workgroup, and every K
-// and V tile loaded into LDS serves all 256 query rows (half the L2 traffic of 128-row workgroups). Causal launches
-// run the late (long) query tiles of every head first.
+// and V tile loaded into LDS serves all 256 query rows (half the L2 traffic of 128-row workgroups). Large launches
+// give each workgroup two query tiles of one head, a late (long) one and an early (short) one, so a causal launch
+// has no tail of short workgroups.
 //
 // Shortcuts. Exact: the row maximum of an unmasked half is taken on the raw scores and scaled once (rounding is
 // monotonic, scale > 0); halves wholly past a wave's last causal row are skipped (their p are exp2(-1e30 - m) = 0
@@ -85,13 +86,14 @@ __device__ __forceinline__ float pair_max(float x) {
   return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
 }
 
+// One query tile `qt` (BQ rows) of head `head`: the whole key pass and the store of its rows. `lds` is the
+// workgroup's ring of K and V tiles; the caller separates two calls with a barrier.
 // `causal` is a run-time argument rather than a template parameter: both variants then get the same code and
 // register allocation, and a non-causal launch only sees its limits at +infinity.
 template <bool BF, int D>
-__global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attention_fwd(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                                                        const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
-                                                        int64_t sq, int64_t sk, float scale, int q_tiles,
-                                                        int causal) {
+__device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                                               const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int64_t sq,
+                                               int64_t sk, float scale, int causal, int qt, int head, uint8_t* lds) {
   static_assert(D == 64 || D == 128, "head dimension 64 or 128");
   constexpr int DCH = D / 8;                // 16-byte chunks per key row
   constexpr int TILE_BYTES = BKEY * D * 2;  // one K (or V) tile
@@ -99,12 +101,7 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
   constexpr int LOADS = BKEY / ROWS_PER_LOAD / FA_WAVES;  // wave load instructions per tile, per operand
   static_assert(LOADS * ROWS_PER_LOAD * FA_WAVES == BKEY, "whole wave loads");
   static_assert(DCH <= 16, "swizzle range");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * TILE_BYTES];
 
-  // Causal: the heavy (late) query tiles of every head first, so the short ones fill the tail of the launch.
-  const int heads = (int)(gridDim.x / q_tiles);
-  const int head = causal ? (int)(blockIdx.x % heads) : (int)(blockIdx.x / q_tiles);
-  const int qt = causal ? (q_tiles - 1 - (int)(blockIdx.x / heads)) : (int)(blockIdx.x % q_tiles);
   const int64_t q0 = (int64_t)qt * BQ;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, half = lane >> 5, r32 = lane & 31;
   const uint16_t* q = Q + (int64_t)head * sq * D;
@@ -118,6 +115,10 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
 #pragma unroll
   for (int s = 0; s < D / 16; ++s)
     qf[s] = qrow < sq ? *reinterpret_cast<const u32x4*>(q + qrow * D + s * 16 + half * 8) : u32x4{};
+  // Q is complete here: the loop's MFMAs read registers that no load is still writing, so the compiler waits for
+  // no load inside the loop (it would otherwise re-check the Q loads before the first score MFMA of every half)
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) asm volatile("" : "+v"(qf[s]));
 
   f32x16 acc[D / 32];
 #pragma unroll
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
       _Pragma("unroll") for (int j = 0; j < LOADS; ++j) {                                                     \
         const int row = (wave * LOADS + j) * ROWS_PER_LOAD + lrow;                                            \
         const int64_t key = min(t0 + row, sk - 1);                                                            \
-        buffer_to_lds16(rsrc, lds + (base) + (wave_s * LOADS + j) * 1024,                                     \
+        buffer_to_lds16(rsrc, lds + (base) + (wave_s * LOADS + j) * 1024,                                       \
                         (uint32_t)(key * D * 2) + (OFF[j] - (uint32_t)(row * D * 2)), 0);                     \
       }                                                                                                       \
     }                                                                                                         \
@@ -337,6 +338,34 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
   }
 }
 
+// The grid. Unpaired: one query tile per workgroup; causal launches run the late (long) tiles of every head first,
+// so the short ones fill the tail. Paired (large launches): workgroup j of a head takes its query tiles
+// q_tiles - 1 - j and then j, so under a causal mask every workgroup has the same number of keys to visit
+// (q_tiles + 1 key tiles of BQ) and the launch has no tail of short workgroups; the middle tile of an odd count
+// runs alone, after all the pairs.
+template <bool BF, int D>
+__global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attention_fwd(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    uint16_t* __restrict__ O, int64_t sq, int64_t sk, float scale, int q_tiles, int causal, int paired) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[5 * BKEY * D * 2];  // three K and two V tiles
+  if (paired) {
+    const int per_head = (q_tiles + 1) / 2;
+    const int heads = (int)(gridDim.x / per_head);
+    const int j = (int)(blockIdx.x / heads), head = (int)(blockIdx.x % heads);
+    const int first = q_tiles - 1 - j;
+    attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, first, head, lds);
+    if (j < first) {
+      __syncthreads();  // every wave is done with the ring before the second tile's loads refill it
+      attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, j, head, lds);
+    }
+    return;
+  }
+  const int heads = (int)(gridDim.x / q_tiles);
+  const int head = causal ? (int)(blockIdx.x % heads) : (int)(blockIdx.x / q_tiles);
+  const int qt = causal ? (q_tiles - 1 - (int)(blockIdx.x / heads)) : (int)(blockIdx.x % q_tiles);
+  attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, qt, head, lds);
+}
+
 }  // namespace krn
 
 using namespace krn;
@@ -345,9 +374,12 @@ template <bool BF, int D>
 static void launch_attention(const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t sq,
                              int64_t sk, float scale, int causal, hipStream_t stream) {
   const int q_tiles = (int)((sq + BQ - 1) / BQ);
-  dim3 grid((unsigned)(bh * q_tiles)), block(64 * FA_WAVES);
+  // pairs when the launch fills the chip twice over even with half the workgroups (256 CUs)
+  const bool paired = q_tiles > 1 && bh * q_tiles >= 2 * 2 * 256;
+  const int64_t blocks = paired ? bh * ((q_tiles + 1) / 2) : bh * q_tiles;
+  dim3 grid((unsigned)blocks), block(64 * FA_WAVES);
   hipLaunchKernelGGL((attention_fwd<BF, D>), grid, block, 0, stream, (const uint16_t*)q, (const uint16_t*)k,
-                     (const uint16_t*)v, (uint16_t*)o, sq, sk, scale, q_tiles, causal);
+                     (const uint16_t*)v, (uint16_t*)o, sq, sk, scale, q_tiles, causal, (int)paired);
 }
 
 extern "C" int krn_attention_fwd(int kind, const void* q, const void* k, const void* v, void* o, int64_t bh,

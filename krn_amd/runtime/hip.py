@@ -25,7 +25,7 @@ from pathlib import Path
 import numpy as np
 
 from krn_amd import dtypes as D
-from krn_amd.compiler import cdna4, hipgen, space
+from krn_amd.compiler import cdna4, dataflow, hipgen, space
 from krn_amd.compiler import ir
 from krn_amd.compiler.capture import TargetError, capture
 from krn_amd.dtypes import Dtype
@@ -365,13 +365,22 @@ class Launch:
 
     def _attention(self, plan: cdna4.AttentionPlan, params: dict, grid: Blocks):
         q, k, v, o = (params[n] for n in (plan.q, plan.k, plan.v, plan.o))
-        bh, sq, d = q.shape
-        sk = k.shape[1]
-        if d != plan.d or k.shape != (bh, sk, d) or v.shape != (bh, sk, d) or o.shape != (bh, sq, d):
+        if len(q.shape) != plan.rank:
             return None
-        if (grid.x, grid.y, grid.z) != (-(-sq // plan.bq), bh, 1) or sk == 0:
+        # (batch, heads, seq, d) tensors are C-contiguous, so they are (batch * heads, seq, d) to the kernel
+        *lead, sq, d = q.shape
+        sk = k.shape[-2]
+        bh = int(np.prod(lead))
+        if d != plan.d or k.shape != (*lead, sk, d) or v.shape != (*lead, sk, d) or o.shape != (*lead, sq, d):
             return None
-        scale = float(np.float32(params[plan.scale]))
+        want = (-(-sq // plan.bq), lead[0], 1) if plan.rank == 3 else (-(-sq // plan.bq), lead[1], lead[0])
+        if (grid.x, grid.y, grid.z) != want or sk == 0:
+            return None
+        value = dataflow.scalar_value(plan.scale, params)
+        if value is None:
+            return None
+        # exp(x) is exp2(x * log2(e)): the kernel's exponent scale carries the base
+        scale = float(np.float32(float(value) * plan.base))
         return lambda stream: library.attention_fwd(plan.dtype, q.pointer, k.pointer, v.pointer, o.pointer, bh, sq,
                                                     sk, d, scale, plan.causal, stream.handle)
 

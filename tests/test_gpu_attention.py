@@ -134,3 +134,40 @@ def test_bf16_flash_attention_with_a_scale_that_is_not_positive(device, factor, 
     scale = factor * math.log2(math.e) / math.sqrt(d)
     want = program_attention(*(bf16_values(w) for w in words), scale, causal)
     np.testing.assert_allclose(run_bf16_attention(device, words, causal, scale, d), want, atol=2e-2)
+
+
+@pytest.mark.parametrize("causal,d,heads,seq,rows,step", [(True, 128, 3, 300, 256, 32), (False, 64, 2, 200, 64, 32)])
+def test_a_rewritten_attention_program_runs_on_the_attention_kernel(device, causal, d, heads, seq, rows, step):
+    """krn's flash attention written another way (names, tiling, temporaries, operand order, the mask as
+    `q_pos >= k_pos`): planned as the attention kernel and equal to a float64 softmax."""
+    from tests.kernels import attention_variants as variants
+
+    rng = np.random.default_rng(7)
+    words = [bf16_words(rng.standard_normal((heads, seq, d)).astype(np.float32)) for _ in range(3)]
+    values = [bf16_values(w) for w in words]
+    o = device.empty(T.bf16, heads, seq, d)
+    shape = variants.Shape(rows_per_block=rows, keys_per_step=step, head_dim=d, masked=causal)
+    args = (shape, *(device.to_device(w, T.bf16) for w in words), o, math.log2(math.e) / math.sqrt(d))
+    launcher = device.launcher(variants.reordered, Blocks(-(-seq // rows), heads))
+    assert launcher.explain(*args)["plan"] == "AttentionPlan"
+    launcher(*args)
+    np.testing.assert_allclose(bf16_values(o.to_host()).astype(np.float64), numpy_attention(*values, causal),
+                               atol=2e-2)
+
+
+def test_a_4d_natural_exp_attention_program_runs_on_the_attention_kernel(device):
+    """(batch, heads, seq, d) tensors indexed by blocks z and y, and `exp` with the plain 1/sqrt(d) scale: the
+    kernel runs it as exp2 with the scale times log2(e)."""
+    from tests.kernels import attention_variants as variants
+
+    batch, heads, seq, d = 2, 3, 260, 128
+    rng = np.random.default_rng(8)
+    words = [bf16_words(rng.standard_normal((batch, heads, seq, d)).astype(np.float32)) for _ in range(3)]
+    values = [bf16_values(w).reshape(batch * heads, seq, d) for w in words]
+    o = device.empty(T.bf16, batch, heads, seq, d)
+    args = (variants.Natural(), *(device.to_device(w, T.bf16) for w in words), o, 1 / math.sqrt(d))
+    launcher = device.launcher(variants.natural_exp_4d, Blocks(-(-seq // 128), heads, batch))
+    assert launcher.explain(*args)["plan"] == "AttentionPlan"
+    launcher(*args)
+    got = bf16_values(o.to_host()).astype(np.float64).reshape(batch * heads, seq, d)
+    np.testing.assert_allclose(got, numpy_attention(*values, True), atol=2e-2)

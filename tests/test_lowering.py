@@ -1,6 +1,8 @@
 """Host-side lowering (no GPU): which gfx950 plan each tile program gets, and the epilogue chain the GEMM plan
 carries to krn_gemm_nt."""
 
+import math
+from pathlib import Path
 import pytest
 
 from krn_amd.compiler import cdna4
@@ -173,3 +175,30 @@ def test_the_generic_mfma_source_compiles_for_gfx950(tmp_path):
     result = subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-c", str(path), "-o", str(tmp_path / "p.o")],
                             capture_output=True, text=True)
     assert result.returncode == 0, result.stderr[-2000:]
+
+
+VARIANTS = Path(__file__).with_name("kernels") / "attention_variants.py"
+
+
+@pytest.mark.parametrize("name,consts,want", [
+    ("reordered", {"cfg": {"rows_per_block": 256, "keys_per_step": 32, "head_dim": 128, "masked": True}},
+     {"q": "query", "k": "key", "v": "value", "o": "out", "bq": 256, "d": 128, "causal": True, "rank": 3}),
+    ("reordered", {"cfg": {"rows_per_block": 64, "keys_per_step": 32, "head_dim": 64, "masked": False}},
+     {"bq": 64, "d": 64, "causal": False, "base": 1.0}),
+    ("natural_exp_4d", {"t": {"bq": 128, "bk": 64, "d": 128, "causal": True}},
+     {"rank": 4, "causal": True, "base": math.log2(math.e)}),
+])
+def test_rewritten_attention_programs_are_recognised_by_their_dataflow(name, consts, want):
+    """Other names, tilings, temporaries, operand orders, mask spellings, the natural exponential and 4-D
+    (batch, heads, seq, d) indexing: the same online softmax, so the same hand-written kernel."""
+    plan = cdna4.lower(capture(VARIANTS, name, consts=consts))
+    assert isinstance(plan, cdna4.AttentionPlan)
+    for field_name, value in want.items():
+        assert getattr(plan, field_name) == value, field_name
+
+
+@pytest.mark.parametrize("name", ["drifting", "unscaled_sum"])
+def test_programs_that_compute_something_else_are_not_taken_for_attention(name):
+    kernel = capture(VARIANTS, name, consts={"t": {"bq": 128, "bk": 64, "d": 128, "causal": True}})
+    assert isinstance(cdna4.lower(kernel), cdna4.GenericPlan)
+    assert any("flash-attention" in reason for reason in cdna4.why_generic(kernel))
