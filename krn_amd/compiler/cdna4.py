@@ -393,9 +393,18 @@ def match_attention(kernel: ir.Kernel) -> AttentionPlan | None:
 
 
 def match_softmax(kernel: ir.Kernel) -> SoftmaxPlan | None:
-    """One of krn's row-softmax programs, recognised like the attention program: the IR compared with the canonical
-    program's IR for the same tiling and element type, after positional renaming."""
-    from krn_amd.compiler import programs
+    """krn's row softmax, recognised by what it computes over x and y of one element type (f16, bf16 or f32, math in
+    float32), with R = `block.tile(R)` rows per block along x:
+
+    * one tile of C columns (reference tests/helpers/example_softmax.py:12-24, `.softmax(axis=1)` or its steps):
+      `y[rows, 0:C] = (e / rowsum(e)).to(dtype)` with `e = exp(v - rowmax(v))`, `v = x[rows, 0:C].to(f32)`;
+    * long rows (reference examples/02_tiles_and_types/01_softmax_rows.py:27-40): a loop over column chunks of x's
+      width carrying a running maximum m (from a constant at or below -3e38) and sum s (from 0), `m' = maximum(m,
+      rowmax(v))`, `s' = s * exp(m - m') + rowsum(exp(v - m'))`, then a loop over the same chunks storing
+      `(exp(v - m) / s).to(dtype)`.
+
+    Names, temporaries and operand order are free; the dataflow is compared, not the spelling."""
+    from krn_amd.compiler import dataflow as df
 
     tensors = [(n, t) for n, t in kernel.params if isinstance(t, ir.TensorType)]
     if len(tensors) != 2 or len(kernel.params) != 2 or any(t.rank != 2 for _, t in tensors):
@@ -403,18 +412,82 @@ def match_softmax(kernel: ir.Kernel) -> SoftmaxPlan | None:
     dtype = tensors[0][1].dtype
     if dtype not in (F16, BF16, F32) or tensors[1][1].dtype != dtype:
         return None
-    consts = dict(kernel.consts)
-    if len(consts) != 1:
+    try:
+        flow = df.evaluate(kernel)
+    except (df.Unsupported, KeyError, IndexError, TypeError):
         return None
-    values = dict(next(iter(consts.values())))
-    if set(values) != {"rows", "cols"} or not all(isinstance(v, int) and v > 0 for v in values.values()):
+    if len(flow.stores) != 1:
         return None
-    form = programs.canonical_form(kernel)
-    for name in programs.SOFTMAX_PROGRAMS:
-        if form == programs.canonical_form(programs.softmax(name, values, dtype)):
-            return SoftmaxPlan(tensors[0][0], tensors[1][0], dtype, int(values["rows"]), int(values["cols"]),
-                               name == "softmax_long_rows")
-    return None
+    y, y_slices, stored = flow.stores[0]
+    if len(y_slices) != 2:
+        return None
+    rows, cols = y_slices
+    r = rows[1]
+    if rows[2] or rows[0] != ("bin", "*", *sorted((("block", "x"), ("const", float(r))), key=repr)):
+        return None
+    if dtype != F32:
+        if stored[0] != "cast" or stored[1] != dtype:
+            return None
+        stored = stored[2]
+
+    def value(load: tuple) -> tuple | None:
+        """v for a load of x at these slices: widened to f32 (f16/bf16) or read as it is (f32)."""
+        inner = load[2] if dtype != F32 and load[0] == "cast" and load[1] == F32 else load
+        if dtype != F32 and inner is load:
+            return None
+        return inner if inner[0] == "load" else None
+
+    if not (stored[0] == "bin" and stored[1] == "/"):
+        return None
+    numerator, denominator = stored[2], stored[3]
+    if not (numerator[0] == "math" and numerator[1] == "exp" and numerator[2][0] == "bin" and numerator[2][1] == "-"):
+        return None
+    v, shift = numerator[2][2], numerator[2][3]
+    load = value(v)
+    if load is None or load[2] != (rows, cols) or load[1] == y:
+        return None
+    x = load[1]
+    if not flow.loops:
+        # one tile: e = exp(v - rowmax(v)), y = e / rowsum(e)
+        if cols[0] != ("const", 0.0) or cols[2] or shift != ("reduce", "max", 1, True, v):
+            return None
+        if denominator != ("reduce", "sum", 1, True, numerator):
+            return None
+        return SoftmaxPlan(x, y, dtype, int(r), int(cols[1]), False)
+    if len(flow.loops) != 2:
+        return None
+    stats, out = flow.loops
+    width = ("dim", x, 1)
+    if not (_const(stats.lo, 0.0) and _const(out.lo, 0.0) and stats.hi == width and out.hi == width and
+            stats.step == out.step == cols[1] and cols[0] == ("loopvar", out.var) and not out.init):
+        return None
+    if set(stats.init) != {shift[1], denominator[1]} or shift[0] != "final" or denominator[0] != "final":
+        return None
+    m, s = shift[1], denominator[1]
+    if not (_fill_at_most(stats.init[m], -3.0e38) and stats.init[s] == ("fill", 0.0, (r, 1))):
+        return None
+    chunk = _substitute_loopvar(v, out.var, stats.var)
+    m_new = ("math", "maximum", *sorted((("state", m), ("reduce", "max", 1, True, chunk)), key=repr))
+    if stats.update[m] != m_new:
+        return None
+    rescaled = ("bin", "*", *sorted((("state", s), ("math", "exp", ("bin", "-", ("state", m), m_new))), key=repr))
+    fresh = ("reduce", "sum", 1, True, ("math", "exp", ("bin", "-", chunk, m_new)))
+    if stats.update[s] != ("bin", "+", *sorted((rescaled, fresh), key=repr)):
+        return None
+    return SoftmaxPlan(x, y, dtype, int(r), int(cols[1]), True)
+
+
+def _fill_at_most(x: tuple, bound: float) -> bool:
+    return x[0] in ("const", "fill") and not isinstance(x[1], bool) and x[1] <= bound
+
+
+def _substitute_loopvar(value, old: str, new: str):
+    """`value` with the loop variable `old` renamed `new` (the same chunk read by another loop)."""
+    if value == ("loopvar", old):
+        return ("loopvar", new)
+    if isinstance(value, tuple):
+        return tuple(_substitute_loopvar(x, old, new) for x in value)
+    return value
 
 
 def lower(kernel: ir.Kernel) -> GemmPlan | AttentionPlan | SoftmaxPlan | GenericPlan:
@@ -434,5 +507,6 @@ def why_generic(kernel: ir.Kernel) -> list[str]:
         reasons.append("not krn's flash-attention program (its dataflow: an online softmax over key tiles with "
                        "exp2 or exp, an optional causal mask, head dimension 64 or 128, f16/bf16 tensors)")
     if match_softmax(kernel) is None:
-        reasons.append("not one of krn's row-softmax programs (compared with the canonical programs' IR)")
+        reasons.append("not krn's row softmax (its dataflow: exp(v - rowmax) / rowsum over one tile, or the running "
+                       "maximum and sum over column chunks; f16, bf16 or f32)")
     return reasons

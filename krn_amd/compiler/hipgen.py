@@ -15,7 +15,7 @@ import math
 from dataclasses import dataclass
 
 from krn_amd.compiler import ir
-from krn_amd.dtypes import BF16, BOOL, F16, F32, F64, I8, I32, I64, PY_FLOAT, PY_INT, Dtype, Kind
+from krn_amd.dtypes import BF16, BOOL, F8E4M3, F16, F32, F64, I8, I32, I64, PY_FLOAT, PY_INT, Dtype, Kind
 
 THREADS = 256
 LDS_LIMIT = 160 * 1024
@@ -50,6 +50,8 @@ PRELUDE = r"""
 typedef unsigned int u32;
 typedef _Float16 _k_half4 __attribute__((ext_vector_type(4)));
 typedef short _k_short4 __attribute__((ext_vector_type(4)));
+typedef _Float16 _k_half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 _k_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float _k_float4 __attribute__((ext_vector_type(4)));
 typedef int _k_int4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float kb16(float x) {
@@ -108,27 +110,35 @@ class MfmaForm:
     integer: bool = False
 
 
+# per operand type, the forms in order of preference: gfx950's 16x16x32 f16/bf16 instructions consume twice the K of
+# the 16x16x16 ones (kept for products whose K is a multiple of 16 only); fp8 e4m3 (the OCP format on gfx950) and
+# int8 consume 32 bytes of K per instruction
 MFMA_FORMS = {
-    F16: MfmaForm("f16", "__builtin_amdgcn_mfma_f32_16x16x16f16", 16, "unsigned short", "_k_half4", "_k_float4"),
-    BF16: MfmaForm("bf16", "__builtin_amdgcn_mfma_f32_16x16x16bf16_1k", 16, "unsigned short", "_k_short4",
-                   "_k_float4"),
-    I8: MfmaForm("i8", "__builtin_amdgcn_mfma_i32_16x16x32_i8", 32, "signed char", "long", "_k_int4", True),
+    F16: (MfmaForm("f16", "__builtin_amdgcn_mfma_f32_16x16x32_f16", 32, "unsigned short", "_k_half8", "_k_float4"),
+          MfmaForm("f16", "__builtin_amdgcn_mfma_f32_16x16x16f16", 16, "unsigned short", "_k_half4", "_k_float4")),
+    BF16: (MfmaForm("bf16", "__builtin_amdgcn_mfma_f32_16x16x32_bf16", 32, "unsigned short", "_k_bf16x8",
+                    "_k_float4"),
+           MfmaForm("bf16", "__builtin_amdgcn_mfma_f32_16x16x16bf16_1k", 16, "unsigned short", "_k_short4",
+                    "_k_float4")),
+    F8E4M3: (MfmaForm("fp8", "__builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8", 32, "unsigned char", "long",
+                      "_k_float4"),),
+    I8: (MfmaForm("i8", "__builtin_amdgcn_mfma_i32_16x16x32_i8", 32, "signed char", "long", "_k_int4", True),),
 }
 
 
 def mfma_form(s: ir.Accumulate) -> MfmaForm | None:
     """The matrix-core instruction for a product, when its operand types have one and the tile extents are whole
     instructions (m and n multiples of 16, k of the instruction's K); None keeps the scalar fused multiply-adds.
-    f16/bf16 products accumulate in float32, int8 ones in int32 (exact, so any order gives the same result)."""
+    f16/bf16/fp8 products accumulate in float32, int8 ones in int32 (exact, so any order gives the same result)."""
     (m, k), n = s.lhs.shape, s.rhs.shape[1]
-    if s.lhs.dtype != s.rhs.dtype or s.lhs.dtype not in MFMA_FORMS:
+    if s.lhs.dtype != s.rhs.dtype or s.lhs.dtype not in MFMA_FORMS or m % 16 or n % 16:
         return None
-    form = MFMA_FORMS[s.lhs.dtype]
-    if (s.acc.dtype == I32) != form.integer or (not form.integer and s.acc.dtype != F32):
-        return None
-    if m % 16 or n % 16 or k % form.k_step:
-        return None
-    return form
+    for form in MFMA_FORMS[s.lhs.dtype]:
+        if (s.acc.dtype == I32) != form.integer or (not form.integer and s.acc.dtype != F32):
+            continue
+        if k % form.k_step == 0:
+            return form
+    return None
 
 
 def products(kernel: ir.Kernel) -> list[str]:
@@ -330,6 +340,7 @@ class Emitter:
         check = f"{valid}[_kk * {rows} + _rr]" if transposed else f"{valid}[_rr * {k} + _kk]"
         bits = {"f16": f"__builtin_bit_cast(unsigned short, (_Float16){source})",
                 "bf16": f"(unsigned short)(__float_as_uint({source}) >> 16)",
+                "fp8": f"(unsigned char){source}",  # the e4m3 code as the tile holds it
                 "i8": f"(signed char){source}"}[form.name]
         self.put(f"for (int _e = threadIdx.x; _e < {rows * k}; _e += {THREADS}) {{")
         self.put(f"  const int _rr = _e / {k}, _kk = _e % {k};")

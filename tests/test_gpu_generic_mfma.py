@@ -29,7 +29,7 @@ def test_partial_k_bf16_gemm_runs_on_mfma(device, m, n, k, kk):
     tiling = programs.PartialK(bm=64, bn=64, bk=32, kk=kk)
     launcher = programs.gemm_partial_k[tiling]
     explained = launcher.explain(a, b, c)
-    assert explained["plan"] == "GenericPlan" and explained["products"] == ["mfma 16x16x16 bf16"]
+    assert explained["plan"] == "GenericPlan" and explained["products"] == ["mfma 16x16x32 bf16"]
     launcher(a, b, c)
     got = c.to_host()
     used = min(kk, k)
@@ -82,7 +82,7 @@ def test_flash_attention_head_dimension_32_runs_on_mfma(device, causal):
     launcher = device.launcher(programs.flash_attention_bf16, launch)
     tensors = [device.to_device(w, T.bf16) for w in words]
     explained = launcher.explain(programs.Attention(**consts), *tensors, o, scale)
-    assert explained["plan"] == "GenericPlan" and explained["products"] == ["mfma 16x16x16 bf16"] * 2
+    assert explained["plan"] == "GenericPlan" and explained["products"] == ["mfma 16x16x32 bf16"] * 2
     assert any("flash-attention" in reason for reason in explained["why"])
     launcher(programs.Attention(**consts), *tensors, o, scale)
     got = bf16_values(o.to_host()).astype(np.float64)
@@ -96,3 +96,30 @@ def test_flash_attention_head_dimension_32_runs_on_mfma(device, causal):
     p = np.exp(scores - scores.max(axis=-1, keepdims=True))
     reference = np.einsum("hqk,hkd->hqd", p / p.sum(axis=-1, keepdims=True), v)
     np.testing.assert_allclose(got, reference, atol=2e-2)
+
+
+def test_fp8_gemm_on_a_larger_grid_runs_on_the_fp8_mfma(device):
+    """An fp8 e4m3 GEMM with per-tensor scales, launched on one block column more than its output: not the
+    whole-product kernel's launch, so the generic lowering runs its product on 16x16x32 fp8 MFMAs (OCP e4m3 on
+    gfx950, the format krn's tensors hold). Checked against the decoded operands in float64."""
+    from krn_amd import Blocks
+    from oracle.numerics import e4m3_decode, e4m3_encode
+
+    m, n, k = 128, 192, 256
+    rng = np.random.default_rng(33)
+    x, w = rng.standard_normal((m, k)).astype(np.float32), rng.standard_normal((n, k)).astype(np.float32)
+    sa, sb = np.float32(np.abs(x).max() / 448), np.float32(np.abs(w).max() / 448)
+    a, b = e4m3_encode(x / sa), e4m3_encode(w / sb)
+    c = device.empty(T.bf16, m, n)
+    tiling = programs.Tiling(bm=64, bn=64, bk=64)
+    launcher = device.launcher(programs.gemm_fp8, Blocks(n // 64 + 1, m // 64))
+    args = (tiling, device.to_device(a, T.f8e4m3fn), device.to_device(b, T.f8e4m3fn), c, sa, sb)
+    explained = launcher.explain(*args)
+    assert explained["plan"] == "GenericPlan" and explained["products"] == ["mfma 16x16x32 fp8"]
+    launcher(*args)
+    got = bf16_values(c.to_host()).astype(np.float64)
+    da, db = e4m3_decode(a).astype(np.float64), e4m3_decode(b).astype(np.float64)
+    scale = np.float64(np.float32(sa * sb))
+    reference = (da @ db.T) * scale
+    bound = (8 * 2.0**-24 * (k + 8) * (np.abs(da) @ np.abs(db).T)) * scale + np.abs(reference) * 2.0**-8 * 1.01
+    assert np.all(np.abs(got - reference) <= bound + 1e-30)

@@ -108,3 +108,19 @@ def test_softmax_programs_take_the_kernel_and_match_the_c_oracle(device, monkeyp
     assert calls[0][4] == width
     np.testing.assert_allclose(decoded(got[:, :width], dtype), decoded(want[:, :width], dtype), rtol=RTOL[dtype],
                                atol=ATOL[dtype])
+
+
+@pytest.mark.parametrize("name,config,rows,cols", [("running", "Rows", 10, 3000), ("one_tile", "Tile", 37, 96)])
+def test_rewritten_softmax_programs_take_the_kernel(device, name, config, rows, cols):
+    """krn's row softmax spelled another way (names, operand order, temporaries): planned as the row-softmax kernel
+    and equal to a float64 softmax of the valid columns."""
+    from tests.kernels import softmax_variants as variants
+
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float16)
+    y = device.empty(T.f16, rows, cols)
+    cfg = getattr(variants, config)()
+    launcher = device.launcher(getattr(variants, name), Blocks(-(-rows // cfg.per_block)))
+    assert launcher.explain(cfg, device.to_device(x), y)["plan"] == "SoftmaxPlan"
+    launcher(cfg, device.to_device(x), y)
+    np.testing.assert_allclose(y.to_host().astype(np.float64), softmax64(x), rtol=RTOL[F16], atol=ATOL[F16])

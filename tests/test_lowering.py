@@ -143,9 +143,11 @@ def test_gemm_launch_marshals_once_and_refuses_partial_grids(monkeypatch):
 
 
 @pytest.mark.parametrize("name, consts, products", [
-    ("gemm_partial_k", {"bm": 64, "bn": 64, "bk": 32, "kk": 96}, ["mfma 16x16x16 bf16"]),
+    ("gemm_partial_k", {"bm": 64, "bn": 64, "bk": 32, "kk": 96}, ["mfma 16x16x32 bf16"]),
+    ("gemm_partial_k", {"bm": 64, "bn": 64, "bk": 16, "kk": 96}, ["mfma 16x16x16 bf16"]),
+    ("gemm_fp8", {"bm": 64, "bn": 64, "bk": 64}, ["mfma 16x16x32 fp8"]),
     ("gemm_i8_partial_k", {"bm": 64, "bn": 64, "bk": 64, "kk": 128}, ["mfma 16x16x32 i8"]),
-    ("flash_attention_bf16", {"bq": 64, "bk": 64, "d": 32, "causal": True}, ["mfma 16x16x16 bf16"] * 2),
+    ("flash_attention_bf16", {"bq": 64, "bk": 64, "d": 32, "causal": True}, ["mfma 16x16x32 bf16"] * 2),
     ("flash_attention", {"bq": 8, "bk": 8, "d": 16, "causal": True}, ["scalar fma"] * 2),
     ("product", {"rows": 8, "cols": 16}, ["scalar fma"]),
 ])  # fmt: skip
@@ -160,7 +162,14 @@ def test_generic_products_take_the_matrix_cores_when_the_tile_extents_allow(name
     assert ("__builtin_amdgcn_mfma" in source) == any(p.startswith("mfma") for p in products)
 
 
-def test_the_generic_mfma_source_compiles_for_gfx950(tmp_path):
+@pytest.mark.parametrize("name,consts,form", [
+    ("gemm_i8_partial_k", {"bm": 64, "bn": 64, "bk": 64, "kk": 128}, "16x16x32 i8"),
+    ("gemm_partial_k", {"bm": 64, "bn": 64, "bk": 32, "kk": 96}, "16x16x32 bf16"),
+    ("gemm_fp8", {"bm": 64, "bn": 64, "bk": 64}, "16x16x32 fp8"),
+    ("matmul", {"bm": 32, "bn": 32, "bk": 32}, "16x16x32 f16"),
+    ("matmul", {"bm": 32, "bn": 32, "bk": 16}, "16x16x16 f16"),
+])
+def test_the_generic_mfma_source_compiles_for_gfx950(tmp_path, name, consts, form):
     """The generated products compile for gfx950 (hipcc cross-compiles here; the GPU tests run them)."""
     import shutil
     import subprocess
@@ -168,7 +177,8 @@ def test_the_generic_mfma_source_compiles_for_gfx950(tmp_path):
     from krn_amd.compiler import hipgen
 
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-    kernel = capture(KERNELS, "gemm_i8_partial_k", consts={"t": {"bm": 64, "bn": 64, "bk": 64, "kk": 128}})
+    kernel = capture(KERNELS, name, consts={"t": consts})
+    assert hipgen.products(kernel) == [f"mfma {form}"]
     source, _ = hipgen.emit(kernel, "krn_probe")
     path = tmp_path / "probe.hip"
     path.write_text("#include <hip/hip_runtime.h>\n" + source)
@@ -202,3 +212,22 @@ def test_programs_that_compute_something_else_are_not_taken_for_attention(name):
     kernel = capture(VARIANTS, name, consts={"t": {"bq": 128, "bk": 64, "d": 128, "causal": True}})
     assert isinstance(cdna4.lower(kernel), cdna4.GenericPlan)
     assert any("flash-attention" in reason for reason in cdna4.why_generic(kernel))
+
+
+SOFTMAXES = Path(__file__).with_name("kernels") / "softmax_variants.py"
+
+
+@pytest.mark.parametrize("name,consts,long_rows", [
+    ("running", {"cfg": {"per_block": 2, "chunk": 256}}, True),
+    ("one_tile", {"cfg": {"per_block": 4, "width": 96}}, False),
+])
+def test_rewritten_softmax_programs_are_recognised_by_their_dataflow(name, consts, long_rows):
+    plan = cdna4.lower(capture(SOFTMAXES, name, consts=consts))
+    assert isinstance(plan, cdna4.SoftmaxPlan) and plan.long_rows == long_rows
+    assert (plan.x, plan.y, plan.rows) == ("src", "dst", next(iter(consts.values()))["per_block"])
+
+
+@pytest.mark.parametrize("name", ["unshifted", "reciprocal"])
+def test_programs_that_round_differently_are_not_taken_for_the_softmax(name):
+    kernel = capture(SOFTMAXES, name, consts={"cfg": {"per_block": 4, "width": 96}})
+    assert isinstance(cdna4.lower(kernel), cdna4.GenericPlan)
