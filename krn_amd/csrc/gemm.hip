@@ -1677,8 +1677,30 @@ static int gemm_dispatch(int fmt, const void* a, const void* b, void* c, int64_t
   const bool mid = piped && t128 <= 256 && 128 * lda <= 0x7fffffff;
   const bool band = piped && fmt != FMT_FP8 && 256 * ldb <= 0x7fffffff;
   const bool large = t256 >= 256 && vec;
+  // A last wave of 256 x 256 tiles at most half full (W8A8 4096 x 14336: 896 tiles, 3.5 waves on 256 CUs) would
+  // leave half the chip idle for a whole tile time. When the full waves cover whole columns of tiles, those
+  // columns run as 256 x 256 tiles and the remaining columns as a second launch of 128 x 256 tiles (twice as many,
+  // half the work each), which fills the last wave. The two launches write disjoint columns of C.
+  const int64_t full_tiles = (t256 / 256) * 256, tile_rows = (m + 255) / 256;
+  const bool split = whole && band && t256 % 256 != 0 && t256 % 256 <= 128 && full_tiles > 0 &&
+                     full_tiles % tile_rows == 0;
+  const int64_t n_split = split ? full_tiles / tile_rows * 256 : 0;
+  Epilogue tail = e;  // the epilogue of the columns from n_split on: column vectors start at that column
+  for (int i = 0; i < e.nops; ++i) {
+    const int op = e.op[i] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[i] >> VEC_KIND_SHIFT;
+    if (op == MUL_COL || op == ADD_COL)
+      tail.vec[i] = static_cast<const uint8_t*>(e.vec[i]) + n_split * (kind == 0 ? 4 : 2);
+  }
+  const int out_bytes = (e.out_kind == F32 || e.out_kind == I32) ? 4 : 2;
+  const void* b_tail = static_cast<const uint8_t*>(b) + n_split * ldb;
+  void* c_tail = static_cast<uint8_t*>(c) + n_split * out_bytes;
 #define KRN_GEMM(F)                                                                                    \
   if (skinny) return launch_skinny<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                \
+  if (split) {                                                                                         \
+    const int rc = launch_whole<F>(a, b, c, m, n_split, kbytes, lda, ldb, ldc, e, stream);             \
+    if (rc != 0) return rc;                                                                            \
+    return launch_band<F>(a, b_tail, c_tail, m, n - n_split, kbytes, lda, ldb, ldc, tail, stream);     \
+  }                                                                                                    \
   if (whole) return launch_whole<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                  \
   if (mid) return launch_mid<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                      \
   if (band) return launch_band<F>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);                    \

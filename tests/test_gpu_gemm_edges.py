@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from krn_amd import T
-from krn_amd.dtypes import BF16, F16, I8
+from krn_amd.dtypes import BF16, F16, F32, I8
 from krn_amd.runtime import hipapi, library
 from oracle.numerics import bf16_values, bf16_words, e4m3_decode, e4m3_encode
 from tests.helpers import agree_bound, assert_agrees
@@ -179,3 +179,36 @@ def test_four_wave_loop_at_its_slice_counts(device, dtype, k_slices):
     out = c.to_host()[rows]
     got = bf16_values(out) if dtype == "bf16" else out.astype(np.float32)
     assert_agrees(got, av[rows], bv.T, k, dtype)
+
+
+def test_w8a8_with_a_half_empty_last_wave_splits_its_columns_bit_exactly(device):
+    """4096 x 4352: 272 tiles of 256 x 256, a last wave of 16 on 256 CUs. The first 4096 columns (256 tiles, one
+    full wave) run as 256 x 256 tiles and the last 256 as 128 x 256 tiles in a second launch, whose per-column
+    scale vector starts at column 4096. int32 accumulation is exact: bf16(f32(f32(acc) * sa[m]) * sw[n])."""
+    m, n, k = 4096, 4352, 128
+    rng = np.random.default_rng(61)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    sa = (rng.uniform(0.5, 1.5, (m, 1)) / 127).astype(np.float32)
+    sw = (rng.uniform(0.5, 1.5, (1, n)) / 127).astype(np.float32)
+    c = device.empty(T.bf16, m, n)
+    programs.gemm_w8a8[programs.Tiling(bm=256, bn=256, bk=128)](device.to_device(a), device.to_device(w),
+                                                               device.to_device(sa), device.to_device(sw), c)
+    acc = (a.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+    np.testing.assert_array_equal(c.to_host(), bf16_words((acc * sa).astype(np.float32) * sw))
+
+
+def test_bf16_with_a_half_empty_last_wave_and_a_column_bias(device):
+    """The same column split for bf16 with a per-column f32 bias added into an f32 result: each column's bias
+    lands on its own column in both launches (within the accumulation bound of float64)."""
+    m, n, k = 4096, 4352, 256
+    rng = np.random.default_rng(62)
+    aw, bw = (bf16_words(rng.standard_normal(s).astype(np.float32)) for s in ((m, k), (n, k)))
+    bias = rng.standard_normal(n).astype(np.float32)
+    a, b, dbias = device.to_device(aw, T.bf16), device.to_device(bw, T.bf16), device.to_device(bias)
+    c = device.empty(T.f32, m, n)
+    library.gemm_nt(BF16, a.pointer, b.pointer, c.pointer, F32, m, n, k, [(library.ADD_COL, 0.0, dbias.pointer)],
+                    device.default_stream.handle)
+    reference, bound = agree_bound(bf16_values(aw), bf16_values(bw).T, k)
+    want = reference + bias.astype(np.float64)
+    assert np.all(np.abs(c.to_host().astype(np.float64) - want) <= bound + np.abs(want) * 2.0**-24)
