@@ -533,11 +533,17 @@ __device__ __forceinline__ int swz4(int row) { return (row >> 2) & 3; }
 // first regrouped per XCD (each XCD gets one contiguous range of tiles and its own L2 sees a compact panel), then
 // ordered in groups of GROUP_M tile rows so neighbours share A rows and B columns.
 __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int& tm, int& tn) {
-  constexpr int GROUP_M = 4;  // bf16 8192^3: 0.5-1.5 % faster than 8 (2: -6 %, 6: -1 %, 16: -9 %); fp8 equal; the
-                              // four-wave loop: 8 equal, 2 -1.5 %
+#ifndef KRN_GROUP_M
+#define KRN_GROUP_M 4
+#endif
+#ifndef KRN_XCD_REMAP
+#define KRN_XCD_REMAP 1
+#endif
+  constexpr int GROUP_M = KRN_GROUP_M;  // bf16 8192^3: 0.5-1.5 % faster than 8 (2: -6 %, 6: -1 %, 16: -9 %); fp8
+                                        // equal; the four-wave loop: 8 equal, 2 -1.5 %
   int nb = tiles_m * tiles_n;
   int bid = blockIdx.x;
-  if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+  if (KRN_XCD_REMAP && nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
   int per_group = GROUP_M * tiles_n;
   int group = bid / per_group;
   int first = group * GROUP_M;
