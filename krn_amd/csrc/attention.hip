@@ -80,10 +80,14 @@ __device__ __forceinline__ int v_slot(int key, int chunk) {
   return D == 128 ? chunk ^ ((key & 3) << 2) : chunk ^ (((key >> 1) & 1) << 2);
 }
 
-// max(x, x of lane ^ 32): the two lanes that hold one query row (v_permlane32_swap, no LDS round trip)
+// max(x, x of lane ^ 32): the two lanes that hold one query row (v_permlane32_swap, no LDS round trip). One
+// v_max_f32 (written as assembly: as fmaxf the compiler first quiets both operands, two more VALU instructions; the
+// instruction quiets a signaling NaN itself, and these operands are arithmetic results or swaps of them).
 __device__ __forceinline__ float pair_max(float x) {
   const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+  float y;
+  asm("v_max_f32 %0, %1, %2" : "=v"(y) : "v"(__uint_as_float(sw[0])), "v"(__uint_as_float(sw[1])));
+  return y;
 }
 
 // One query tile `qt` (BQ rows) of head `head`: the whole key pass and the store of its rows. `lds` is the
@@ -200,7 +204,7 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
       _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                         \
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(S[step * 8 + 2 * j], sc, neg_m));              \
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(S[step * 8 + 2 * j + 1], sc, neg_m));          \
-        psum[step] += p0 + p1;                                                                                \
+        psum[step] = j == 0 ? p0 + p1 : psum[step] + (p0 + p1); /* no 0 + x: -0 keeps it from folding */     \
         w[j] = Half<BF>::pack(p0, p1);                                                                        \
       }                                                                                                       \
       pf[step] = u32x4{w[0], w[1], w[2], w[3]};                                                               \
@@ -282,7 +286,7 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
       }                                                                                                       \
       /* masked halves already hold scaled scores: one fused multiply-add serves both (x * 1 - m is exact) */ \
       const float sc = masked ? 1.0f : scale;                                                                 \
-      float psum[2] = {0.0f, 0.0f};                                                                           \
+      float psum[2];                                                                                          \
       u32x4 pf[2];                                                                                            \
       if (next) {                                                                                             \
         if ((hb) == 0) KRN_FA_SCORES(SN, kcur, 1);                                                            \
