@@ -171,3 +171,23 @@ def test_a_4d_natural_exp_attention_program_runs_on_the_attention_kernel(device)
     launcher(*args)
     got = bf16_values(o.to_host()).astype(np.float64).reshape(batch * heads, seq, d)
     np.testing.assert_allclose(got, numpy_attention(*values, True), atol=2e-2)
+
+
+def test_a_4d_attention_program_the_kernel_does_not_serve_runs_generically(device):
+    """Head dimension 32 is outside the attention kernel: the same 4-D program lowers to generated HIP (two
+    16x16x32 bf16 MFMA products, blocks over x, y and z) and still equals the float64 softmax."""
+    from tests.kernels import attention_variants as variants
+
+    batch, heads, seq, d = 2, 2, 130, 32
+    rng = np.random.default_rng(9)
+    words = [bf16_words(rng.standard_normal((batch, heads, seq, d)).astype(np.float32)) for _ in range(3)]
+    values = [bf16_values(w).reshape(batch * heads, seq, d) for w in words]
+    o = device.empty(T.bf16, batch, heads, seq, d)
+    cfg = variants.Natural(bq=64, bk=64, d=d, causal=True)
+    args = (cfg, *(device.to_device(w, T.bf16) for w in words), o, 1 / math.sqrt(d))
+    launcher = device.launcher(variants.natural_exp_4d, Blocks(-(-seq // 64), heads, batch))
+    explained = launcher.explain(*args)
+    assert explained["plan"] == "GenericPlan" and explained["products"] == ["mfma 16x16x32 bf16"] * 2
+    launcher(*args)
+    got = bf16_values(o.to_host()).astype(np.float64).reshape(batch * heads, seq, d)
+    np.testing.assert_allclose(got, numpy_attention(*values, True), atol=2e-2)
