@@ -91,13 +91,18 @@ __device__ __forceinline__ float pair_max(float x) {
 }
 
 // One query tile `qt` (BQ rows) of head `head`: the whole key pass and the store of its rows. `lds` is the
-// workgroup's ring of K and V tiles; the caller separates two calls with a barrier.
+// workgroup's ring of K and V tiles. `qf` holds this lane's Q fragments: loaded here unless `preloaded`, in which
+// case the previous tile of the same head has already loaded them and issued this tile's first K and V loads.
+// `next_qt` (or -1) is the query tile this workgroup takes next in the same head: once the key loop's last
+// barrier has passed (every wave is done with the ring), its first K and V tiles and its Q fragments are loaded
+// before this tile's epilogue, so their latency runs under the epilogue instead of at the next tile's start.
 // `causal` is a run-time argument rather than a template parameter: both variants then get the same code and
 // register allocation, and a non-causal launch only sees its limits at +infinity.
 template <bool BF, int D>
 __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                                                const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int64_t sq,
-                                               int64_t sk, float scale, int causal, int qt, int head, uint8_t* lds) {
+                                               int64_t sk, float scale, int causal, int qt, int head, uint8_t* lds,
+                                               u32x4 (&qf)[D / 16], bool preloaded, int next_qt) {
   static_assert(D == 64 || D == 128, "head dimension 64 or 128");
   constexpr int DCH = D / 8;                // 16-byte chunks per key row
   constexpr int TILE_BYTES = BKEY * D * 2;  // one K (or V) tile
@@ -115,10 +120,11 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
 
   // this lane's query row and its Q fragments (B operand of S^T = K Q^T): 8 contiguous d per MFMA step
   const int64_t qrow = q0 + wave * 32 + r32;
-  u32x4 qf[D / 16];
+  if (!preloaded) {
 #pragma unroll
-  for (int s = 0; s < D / 16; ++s)
-    qf[s] = qrow < sq ? *reinterpret_cast<const u32x4*>(q + qrow * D + s * 16 + half * 8) : u32x4{};
+    for (int s = 0; s < D / 16; ++s)
+      qf[s] = qrow < sq ? *reinterpret_cast<const u32x4*>(q + qrow * D + s * 16 + half * 8) : u32x4{};
+  }
   // Q is complete here: the loop's MFMAs read registers that no load is still writing, so the compiler waits for
   // no load inside the loop (it would otherwise re-check the Q loads before the first score MFMA of every half)
 #pragma unroll
@@ -241,9 +247,11 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
   f32x16 sa, sb;
   float tmax_next = -INFINITY;  // the scaled row maximum of the next half's raw scores
   if (ntiles > 0) {
-    KRN_FA_LOAD(k_rsrc, 0, 0, koff);
-    KRN_FA_LOAD(v_rsrc, 0, V_BASE, voff);
-    if (ntiles > 1) KRN_FA_LOAD(k_rsrc, 1, TILE_BYTES, koff);
+    if (!preloaded) {
+      KRN_FA_LOAD(k_rsrc, 0, 0, koff);
+      KRN_FA_LOAD(v_rsrc, 0, V_BASE, voff);
+      if (ntiles > 1) KRN_FA_LOAD(k_rsrc, 1, TILE_BYTES, koff);
+    }
     KRN_FA_PUBLISH();
     KRN_FA_SCORES(sa, 0, 0);  // the first half is active for every wave
     KRN_FA_RAWMAX(sa, tmax_next);
@@ -315,6 +323,19 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
     KRN_FA_PUBLISH();
     kcur = knext;
   }
+  if (next_qt >= 0) {
+    // the ring is free (every wave has passed the loop's last barrier): the next tile's first K and V tiles and
+    // its Q fragments (this tile's are dead) go out now
+    const int64_t next_q0 = (int64_t)next_qt * BQ;
+    const int64_t next_kend = causal ? min(sk, next_q0 + BQ) : sk;
+    KRN_FA_LOAD(k_rsrc, 0, 0, koff);
+    KRN_FA_LOAD(v_rsrc, 0, V_BASE, voff);
+    if (next_kend > BKEY) KRN_FA_LOAD(k_rsrc, 1, TILE_BYTES, koff);
+    const int64_t next_row = next_q0 + wave * 32 + r32;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s)
+      qf[s] = next_row < sq ? *reinterpret_cast<const u32x4*>(q + next_row * D + s * 16 + half * 8) : u32x4{};
+  }
 #undef KRN_FA_LOAD
 #undef KRN_FA_PUBLISH
 #undef KRN_FA_SCORES
@@ -357,17 +378,16 @@ __global__ __launch_bounds__(64 * FA_WAVES, 512 / (64 * FA_WAVES)) void attentio
     const int heads = (int)(gridDim.x / per_head);
     const int j = (int)(blockIdx.x / heads), head = (int)(blockIdx.x % heads);
     const int first = q_tiles - 1 - j;
-    attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, first, head, lds);
-    if (j < first) {
-      __syncthreads();  // every wave is done with the ring before the second tile's loads refill it
-      attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, j, head, lds);
-    }
+    u32x4 qf[D / 16];
+    attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, first, head, lds, qf, false, j < first ? j : -1);
+    if (j < first) attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, j, head, lds, qf, true, -1);
     return;
   }
   const int heads = (int)(gridDim.x / q_tiles);
   const int head = causal ? (int)(blockIdx.x % heads) : (int)(blockIdx.x / q_tiles);
   const int qt = causal ? (q_tiles - 1 - (int)(blockIdx.x / heads)) : (int)(blockIdx.x % q_tiles);
-  attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, qt, head, lds);
+  u32x4 qf[D / 16];
+  attention_tile<BF, D>(Q, K, V, O, sq, sk, scale, causal, qt, head, lds, qf, false, -1);
 }
 
 }  // namespace krn
