@@ -350,17 +350,32 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
     total = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
   const float inv = 1.0f / total;  // one division per row instead of 64 per lane (causal B4 H32 S4096 D128 +2 %)
-  if (qrow < sq) {
+  // Lane (r32, half) holds columns i * 32 + gq * 8 + half * 4 .. + 3 of its row; its partner lane ^ 32 the other
+  // four of each group of eight. One v_permlane32_swap per word pairs them, so that the lower lane owns the eight
+  // columns of the even groups and the upper lane those of the odd ones: every store is 16 bytes, and one store
+  // instruction writes 32 contiguous bytes of each of 32 rows (8 stores per lane instead of 16 of 8 bytes).
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i)
+  for (int i = 0; i < D / 32; ++i)
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int d = i * 32 + gq * 8 + half * 4;
-        const uint32_t lo = Half<BF>::pack(acc[i][gq * 4 + 0] * inv, acc[i][gq * 4 + 1] * inv);
-        const uint32_t hi = Half<BF>::pack(acc[i][gq * 4 + 2] * inv, acc[i][gq * 4 + 3] * inv);
-        *reinterpret_cast<uint2*>(o + qrow * D + d) = uint2{lo, hi};
+    for (int gp = 0; gp < 2; ++gp) {
+      uint32_t w[2][2];  // [group gq = 2 gp + e][word]: this lane's four columns of each of the two groups
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2) {
+        const int gq = 2 * gp + e2;
+        w[e2][0] = Half<BF>::pack(acc[i][gq * 4 + 0] * inv, acc[i][gq * 4 + 1] * inv);
+        w[e2][1] = Half<BF>::pack(acc[i][gq * 4 + 2] * inv, acc[i][gq * 4 + 3] * inv);
       }
-  }
+      // the lower lane gives away its odd group, the upper lane its even group
+      uint32_t got[2];
+#pragma unroll
+      for (int word = 0; word < 2; ++word) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(w[0][word], w[1][word], false, false);
+        got[word] = half ? sw[0] : sw[1];
+      }
+      const int e2 = half;  // the group this lane stores
+      const uint4 piece = half ? uint4{got[0], got[1], w[1][0], w[1][1]} : uint4{w[0][0], w[0][1], got[0], got[1]};
+      if (qrow < sq) *reinterpret_cast<uint4*>(o + qrow * D + i * 32 + (2 * gp + e2) * 8) = piece;
+    }
 }
 
 // The grid. Unpaired: one query tile per workgroup; causal launches run the late (long) tiles of every head first,
