@@ -100,6 +100,86 @@ struct Mfma<FMT_FP8> {
   }
 };
 
+// The 16x16 forms, which consume twice the K per instruction for 16-bit and int8 operands. On gfx950 they sustain
+// more throughput than the 32x32 forms under the same power limit (MFMA-only loops on random operands: bf16
+// 16x16x32 0.93 of the per-clock peak at 1.71 GHz against 0.84 at 1.62 GHz for 32x32x16; int8 16x16x64 0.95 at
+// 1.79 GHz against 0.85 at 1.59 GHz). Operand lane L holds row (or column) L & 15 and 16 bytes of K from
+// (L >> 4) * 16; accumulator lane L holds column L & 15 of rows 4 (L >> 4) .. + 3.
+template <int FMT>
+struct Mfma16;
+
+template <>
+struct Mfma16<FMT_BF16> {
+  typedef f32x4 Acc;
+  __device__ static void step(Acc& c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                0, 0);
+  }
+  // the same as assembly with the accumulator tied to one AGPR tuple (the allocator otherwise moves 4-register
+  // accumulators between AGPRs and VGPRs around the loop)
+  __device__ static void step_agpr(Acc& c, u32x4 a, u32x4 b) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+};
+
+template <>
+struct Mfma16<FMT_F16> {
+  typedef f32x4 Acc;
+  __device__ static void step(Acc& c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                               0);
+  }
+  __device__ static void step_agpr(Acc& c, u32x4 a, u32x4 b) {
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+};
+
+template <>
+struct Mfma16<FMT_I8> {
+  typedef i32x4 Acc;
+  __device__ static void step(Acc& c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
+                                              0);
+  }
+  __device__ static void step_agpr(Acc& c, u32x4 a, u32x4 b) {
+    asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+};
+
+// Four 16x16 accumulator blocks s[R][C] (rows 16 R, columns 16 C of a 32 x 32 block) in the layout of one 32x32
+// accumulator, so that every store path serves both forms. Target lane L = (h5, h4, low4) register
+// 8 R + 4 b + q holds row 8 (2 R + b) + 4 h5 + q, column 16 h4 + low4: that is register q of block s[R][h4] at lane
+// (b, h5, low4). Per pair of source registers (the same q of s[R][0] and s[R][1], as 16-lane rows [a0 a1 a2 a3] and
+// [b0 b1 b2 b3]) a v_permlane16_swap gives [a0 b0 a2 b2] and [a1 b1 a3 b3], and a v_permlane32_swap of those gives
+// [a0 b0 a1 b1] (b = 0) and [a2 b2 a3 b3] (b = 1).
+template <typename V>
+struct Elem;
+template <>
+struct Elem<f32x16> {
+  typedef float T;
+};
+template <>
+struct Elem<i32x16> {
+  typedef int T;
+};
+
+template <typename V16, typename V4>
+__device__ __forceinline__ V16 join16(const V4& s00, const V4& s01, const V4& s10, const V4& s11) {
+  V16 t;
+#pragma unroll
+  for (int R = 0; R < 2; ++R)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t x0 = __builtin_bit_cast(uint32_t, R ? s10[q] : s00[q]);
+      const uint32_t x1 = __builtin_bit_cast(uint32_t, R ? s11[q] : s01[q]);
+      const auto p = __builtin_amdgcn_permlane16_swap(x0, x1, false, false);
+      const auto w = __builtin_amdgcn_permlane32_swap(p[0], p[1], false, false);
+      t[8 * R + q] = __builtin_bit_cast(typename Elem<V16>::T, (uint32_t)w[0]);
+      t[8 * R + 4 + q] = __builtin_bit_cast(typename Elem<V16>::T, (uint32_t)w[1]);
+    }
+  return t;
+}
+
 // Store one 32x32 accumulator block (the C layout of a 32x32 MFMA: lane holds column lane & 31 and rows
 // (r/4)*8 + (lane/32)*4 + r%4) through a per-wave LDS patch with a 36-word row stride, so that each lane then owns
 // 16 consecutive elements of one row: lane l takes row l/2, columns (l&1)*16 .. +16, applies the epilogue and
@@ -437,14 +517,15 @@ template <typename V>
 __device__ __forceinline__ V agpr_block(const V& x) {
   V y;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(y[r]) : "a"(x[r]) : "memory");
+  for (int r = 0; r < (int)(sizeof(V) / 4); ++r)
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(y[r]) : "a"(x[r]) : "memory");
   return y;
 }
 
-template <bool INT, int TM, int TN, typename Acc, bool AGPR = false>
-__device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* patch, void* C, int64_t ldc,
-                                           int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
-                                           int lane) {
+// `fetch(i, j)` hands over block (i, j) in the 32x32 accumulator layout; AGPR: blocks are stored in pairs.
+template <bool INT, int TM, int TN, bool AGPR, typename Fetch>
+__device__ __forceinline__ void store_tile_by(Fetch fetch, uint32_t* patch, void* C, int64_t ldc, int64_t row0,
+                                              int64_t col0, int64_t M, int64_t N, const Epilogue& e, int lane) {
   const bool direct = direct_epilogue(e) && (ldc % 2) == 0 && (uintptr_t)C % 4 == 0 && row0 + 32 * TM <= M &&
                       col0 + 32 * TN <= N && (int64_t)32 * TM * ldc * 2 <= 0x7fffffff;
   if (direct) {
@@ -470,11 +551,10 @@ __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* p
   _Pragma("unroll") for (int i = 0; i < TM; ++i) {                                                           \
     if constexpr (AGPR) {                                                                                    \
       _Pragma("unroll") for (int j = 0; j < TN; j += 2)                                                      \
-        store_pair_direct<INT, BF>(agpr_block(acc[i][j]), agpr_block(acc[i][j + 1]), dv, i, j, out,          \
-                                   lane_off, ldc, e, lane);                                                  \
+        store_pair_direct<INT, BF>(fetch(i, j), fetch(i, j + 1), dv, i, j, out, lane_off, ldc, e, lane);     \
     } else {                                                                                                 \
       _Pragma("unroll") for (int j = 0; j < TN; ++j)                                                         \
-        store_block_direct<INT, BF>(acc[i][j], dv, i, j, out, lane_off, ldc, e, lane);                       \
+        store_block_direct<INT, BF>(fetch(i, j), dv, i, j, out, lane_off, ldc, e, lane);                     \
     }                                                                                                        \
   }
     if (e.out_kind == BF16) {
@@ -492,11 +572,34 @@ __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* p
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-      if constexpr (AGPR)
-        store_block<INT>(agpr_block(acc[i][j]), patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, local, lane);
-      else
-        store_block<INT>(acc[i][j], patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, local, lane);
+    for (int j = 0; j < TN; ++j) store_block<INT>(fetch(i, j), patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, local, lane);
+}
+
+template <bool INT, int TM, int TN, typename Acc, bool AGPR = false>
+__device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* patch, void* C, int64_t ldc,
+                                           int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
+                                           int lane) {
+  store_tile_by<INT, TM, TN, AGPR>(
+      [&](int i, int j) {
+        if constexpr (AGPR)
+          return agpr_block(acc[i][j]);
+        else
+          return acc[i][j];
+      },
+      patch, C, ldc, row0, col0, M, N, e, lane);
+}
+
+// The same for 2 TM x 2 TN blocks of 16 x 16 in AGPRs, joined into 32x32 blocks as they are stored.
+template <bool INT, int TM, int TN, typename V16, typename V4>
+__device__ __forceinline__ void store_tile16(const V4 (&acc)[2 * TM][2 * TN], uint32_t* patch, void* C, int64_t ldc,
+                                             int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
+                                             int lane) {
+  store_tile_by<INT, TM, TN, true>(
+      [&](int i, int j) {
+        return join16<V16>(agpr_block(acc[2 * i][2 * j]), agpr_block(acc[2 * i][2 * j + 1]),
+                           agpr_block(acc[2 * i + 1][2 * j]), agpr_block(acc[2 * i + 1][2 * j + 1]));
+      },
+      patch, C, ldc, row0, col0, M, N, e, lane);
 }
 
 // 16 bytes of row `base` starting at byte `kb`, zero past the row's end or for a row outside the matrix. VEC: the
@@ -996,7 +1099,6 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
     for (int c = 0; c < CH; ++c) rd[s][c] = r32 * 128 + ((((2 * s + half) * CH + c) ^ sw) * 16);
   const int wr = wave * 8192 + lane * 16;
   const int nk = (int)(kbytes / BKB);  // >= 2 (host)
-
   // register sets of one slice of this wave's rows each (0-7 A, 8-15 B): with two, a slice is loaded two slices
   // before it is written to LDS, which covers an L2 miss under load (about 3000 cycles against 2048 per slice);
   // fp8's fragments take the registers of a second set
@@ -1189,6 +1291,233 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
   __syncthreads();  // every wave is done with the stages before its LDS becomes the store patches
   uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
   store_tile<FMT == FMT_I8, 4, 4, Acc, true>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
+}
+
+#ifndef KRN_D16_NOLOAD
+#define KRN_D16_NOLOAD 0
+#endif
+// Four-wave main loop for whole 256 x 256 tiles of 16-bit operands (NT) with the 16x16x32 MFMA form and
+// direct-to-LDS slices. Each wave owns a 128 x 128 quarter (wave w: rows 128 (w >> 1), columns 128 (w & 1)) as
+// 8 x 8 accumulator blocks of 16 x 16 in AGPRs. 128-byte K slices go straight from global memory into LDS stages, NA
+// for A and NB for B (2 or 3; 3 + 2 stages of 32 KiB fill the 160 KiB), each stage a separate array so that the
+// compiler can tell every fragment read from the loads in flight into the other stages; wave w loads rows
+// 64 w .. 64 w + 63 of A and of B, 8 rows (1 KiB) per load, chunk c of row r at slot c ^ ((r >> 1) & 7).
+//
+// A slice is two steps of 32 K. One set of fragments (A blocks 0-3 and B blocks 0-3, each two 16-row halves) is
+// refilled in place: step 0 runs its 16 blocks of 32 x 32 row by row (block (I, J) is group 4 I + J of four
+// MFMAs), step 1 column by column, so a block's fragments are dead after its last group of the step and take the
+// next step's at once (step 0 frees A block I after group 4 I + 3 and B block J after 12 + J; step 1 frees B block
+// J after 4 J + 3 and A block I after 12 + I). The one barrier per slice sits after group 3 of step 1: by then
+// this wave has read all of slice kt (its step-1 fragments were read during step 0) and its loads of slice kt + 1
+// have landed; after it the loads of slice kt + N of an operand with N stages go into the stage slice kt leaves,
+// and the fragments of slice kt + 1 are read as step 1 frees their registers. An operand's slice thus has N - 1
+// slices of MFMA time to arrive.
+template <int FMT, int NA = 2, int NB = 2>
+__global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+                                                     void* __restrict__ C, int64_t M, int64_t N, int64_t kbytes,
+                                                     int64_t lda, int64_t ldb, int64_t ldc, Epilogue e) {
+  static_assert((NA == 2 || NA == 3) && (NB == 2 || NB == 3) && NA + NB <= 5, "stages: 160 KiB of LDS");
+  typedef Mfma16<FMT> Unit;
+  typedef typename Unit::Acc Acc;
+  typedef typename Mfma<FMT>::Acc Acc32;
+  constexpr int BM = 256, BN = 256, BKB = 128;
+  constexpr int HALF = BM * BKB;  // 32 KiB: one operand's rows of one slice
+  constexpr int UNROLL = NA == NB ? 2 : 6;  // slices per loop iteration: every stage index a constant
+  __shared__ __attribute__((aligned(1024))) uint8_t la0[HALF];
+  __shared__ __attribute__((aligned(1024))) uint8_t la1[HALF];
+  __shared__ __attribute__((aligned(1024))) uint8_t la2[NA == 3 ? HALF : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t lb0[HALF];
+  __shared__ __attribute__((aligned(1024))) uint8_t lb1[HALF];
+  __shared__ __attribute__((aligned(1024))) uint8_t lb2[NB == 3 ? HALF : 16];
+  int tm, tn;
+  tile_of((int)((M + BM - 1) / BM), (int)((N + BN - 1) / BN), tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  auto uniform = [](const void* p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const void*)(((uint64_t)hi << 32) | lo);
+  };
+  const int64_t a_bytes = __builtin_amdgcn_readfirstlane((int)min((M - m0) * lda, (int64_t)0x7fffffff));
+  const int64_t b_bytes = __builtin_amdgcn_readfirstlane((int)min((N - n0) * ldb, (int64_t)0x7fffffff));
+  const __amdgpu_buffer_rsrc_t a_rsrc = panel_rsrc(uniform(A + m0 * lda), a_bytes),
+                              b_rsrc = panel_rsrc(uniform(B + n0 * ldb), b_bytes);
+  // load item j of an operand: rows 64 wave + 8 j .. + 7; lane i takes row i / 8 and the global chunk that belongs at
+  // slot i % 8. The swizzle of row 8 j + i / 8 depends on j only through j & 1.
+  const int lrow = lane >> 3, lslot = lane & 7;
+  uint32_t ga[2], gb[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int row = wave * 64 + p * 8 + lrow;
+    ga[p] = (uint32_t)(row * lda + ((lslot ^ swz8(row)) * 16));
+    gb[p] = (uint32_t)(row * ldb + ((lslot ^ swz8(row)) * 16));
+  }
+  const int wbase = wave * 8192;
+  // fragment bases: lane L reads row L & 15 of a 16-row half, 16-byte chunk 4 s + (L >> 4) (step s)
+  int ra[2], rb[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int part = (lane & 15) * 128 + (((4 * s + (lane >> 4)) ^ (((lane & 15) >> 1) & 7)) * 16);
+    ra[s] = part + wm * 128 * 128;
+    rb[s] = part + wn * 128 * 128;
+  }
+  const int nk = (int)(kbytes / BKB);  // >= 2 (host)
+
+  u32x4 F[16];  // A block I half R at 2 I + R, B block J half Q at 8 + 2 J + Q
+  Acc acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = Acc{};
+
+#define KD_A(p) ((p) == 0 ? la0 : (p) == 1 ? la1 : la2)
+#define KD_B(p) ((p) == 0 ? lb0 : (p) == 1 ? lb1 : lb2)
+#define KD_LOADA(j, sl, pa)                                                                                    \
+  buffer_to_lds16(a_rsrc, KD_A(pa) + wbase + (j) * 1024, ga[(j) & 1], (int)((sl) * BKB + ((j) & 6) * 8 * lda))
+#define KD_LOADB(j, sl, pb)                                                                                    \
+  buffer_to_lds16(b_rsrc, KD_B(pb) + wbase + (j) * 1024, gb[(j) & 1], (int)((sl) * BKB + ((j) & 6) * 8 * ldb))
+#define KD_READ(r, c, pa, pb, s)                                                                               \
+  F[(r) * 2 + (c)] = *reinterpret_cast<const u32x4*>(                                                          \
+      ((r) < 4 ? KD_A(pa) + ra[s] : KD_B(pb) + rb[s]) + (((r) & 3) * 32 + (c) * 16) * 128)
+#define KD_FENCE() __builtin_amdgcn_sched_barrier(0)
+#define KD_MMA(m)                                                                                              \
+  _Pragma("unroll") for (int R = 0; R < 2; ++R) _Pragma("unroll") for (int Q = 0; Q < 2; ++Q)                 \
+      Unit::step_agpr(acc[((m) >> 2) * 2 + R][((m) & 3) * 2 + Q], F[((m) >> 2) * 2 + R], F[8 + ((m) & 3) * 2 + Q])
+  // step 0 of slice kt (A stage PA, B stage PB): its groups row by row; the step-1 fragments as registers free up
+#define KD_STEP0(PA, PB)                                                                                       \
+  do {                                                                                                         \
+    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
+      KD_MMA(m);                                                                                               \
+      KD_FENCE();                                                                                              \
+      if ((m & 3) == 3) {                                                                                      \
+        KD_READ(m >> 2, 0, PA, PB, 1);                                                                         \
+        KD_READ(m >> 2, 1, PA, PB, 1);                                                                         \
+        KD_FENCE();                                                                                            \
+      }                                                                                                        \
+      if ((m >> 2) == 3) {                                                                                     \
+        KD_READ(4 + (m & 3), 0, PA, PB, 1);                                                                    \
+        KD_READ(4 + (m & 3), 1, PA, PB, 1);                                                                    \
+        KD_FENCE();                                                                                            \
+      }                                                                                                        \
+    }                                                                                                          \
+  } while (0)
+  // step 1 of slice kt: column by column. After group 3 the barrier (this wave's loads of slice kt + 1 landed: only
+  // the loads of a three-stage operand's slice kt + 2, issued last, may still be in flight), then the loads into the
+  // stages slice kt leaves, two-stage operands first (past the end: the last slice again, into a stage nothing
+  // reads any more), and the step-0 fragments of slice kt + 1
+#define KD_STEP1(PA, PB, kt)                                                                                   \
+  do {                                                                                                         \
+    _Pragma("unroll") for (int g = 0; g < 16; ++g) {                                                           \
+      KD_MMA((g & 3) * 4 + (g >> 2));                                                                          \
+      KD_FENCE();                                                                                              \
+      if (g == 3) {                                                                                            \
+        if constexpr (NA == 3 || NB == 3)                                                                      \
+          __builtin_amdgcn_s_waitcnt(0x0070 | 8); /* vmcnt(8) lgkmcnt(0) */                                     \
+        else                                                                                                   \
+          __builtin_amdgcn_s_waitcnt(0x0070); /* vmcnt(0) lgkmcnt(0) */                                         \
+        __builtin_amdgcn_s_barrier();                                                                          \
+        KD_FENCE();                                                                                            \
+      }                                                                                                        \
+      if (!KRN_D16_NOLOAD && g >= 3 && g < 11) {                                                               \
+        const int j = 2 * (g - 3);                                                                             \
+        if (j < 8) {                                                                                           \
+          if constexpr (NB <= NA) {                                                                            \
+            KD_LOADB(j, min((kt) + NB, nk - 1), PB);                                                       \
+            KD_LOADB(j + 1, min((kt) + NB, nk - 1), PB);                                                   \
+          } else {                                                                                             \
+            KD_LOADA(j, min((kt) + NA, nk - 1), PA);                                                       \
+            KD_LOADA(j + 1, min((kt) + NA, nk - 1), PA);                                                   \
+          }                                                                                                    \
+        } else {                                                                                               \
+          if constexpr (NB <= NA) {                                                                            \
+            KD_LOADA(j - 8, min((kt) + NA, nk - 1), PA);                                                   \
+            KD_LOADA(j - 7, min((kt) + NA, nk - 1), PA);                                                   \
+          } else {                                                                                             \
+            KD_LOADB(j - 8, min((kt) + NB, nk - 1), PB);                                                   \
+            KD_LOADB(j - 7, min((kt) + NB, nk - 1), PB);                                                   \
+          }                                                                                                    \
+        }                                                                                                      \
+        KD_FENCE();                                                                                            \
+      }                                                                                                        \
+      if ((g & 3) == 3) {                                                                                      \
+        KD_READ(4 + (g >> 2), 0, ((PA) + 1) % NA, ((PB) + 1) % NB, 0);                                          \
+        KD_READ(4 + (g >> 2), 1, ((PA) + 1) % NA, ((PB) + 1) % NB, 0);                                          \
+        KD_FENCE();                                                                                            \
+      }                                                                                                        \
+      if ((g >> 2) == 3) {                                                                                     \
+        KD_READ(g & 3, 0, ((PA) + 1) % NA, ((PB) + 1) % NB, 0);                                                 \
+        KD_READ(g & 3, 1, ((PA) + 1) % NA, ((PB) + 1) % NB, 0);                                                 \
+        KD_FENCE();                                                                                            \
+      }                                                                                                        \
+    }                                                                                                          \
+  } while (0)
+#define KD_SLICE(u, kt)                                                                                        \
+  do {                                                                                                         \
+    KD_STEP0((u) % NA, (u) % NB);                                                                              \
+    KD_STEP1((u) % NA, (u) % NB, kt);                                                                          \
+  } while (0)
+
+  // the prologue: the first NA slices of A and NB of B, slice by slice (a three-stage operand's third slice last,
+  // as in the loop); once slice 0 has landed everywhere, its step-0 fragments
+#pragma unroll
+  for (int sl = 0; sl < 3; ++sl) {
+    if (sl < NA - (NA == 3)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) KD_LOADA(j, min(sl, nk - 1), sl);
+    }
+    if (sl < NB - (NB == 3)) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) KD_LOADB(j, min(sl, nk - 1), sl);
+    }
+  }
+  if constexpr (NA == 3) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) KD_LOADA(j, min(2, nk - 1), 2);
+  }
+  if constexpr (NB == 3) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) KD_LOADB(j, min(2, nk - 1), 2);
+  }
+  // slice 0's 16 loads came first
+  __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | (NA + NB == 5 ? 24 : 16));
+  __builtin_amdgcn_s_barrier();
+  KD_FENCE();
+  // in the order step 1 reads them (B0 B1 B2 A0 A1 A2 B3 A3), so that the loop's first MFMAs wait on the same
+  // partial LDS count whether they follow this or the loop's last step
+#pragma unroll
+  for (int x = 0; x < 8; ++x) {
+    const int r = x < 3 ? 4 + x : x < 6 ? x - 3 : x == 6 ? 7 : 3;
+    KD_READ(r, 0, 0, 0, 0);
+    KD_READ(r, 1, 0, 0, 0);
+    KD_FENCE();
+  }
+  int kt = 0;
+  for (; kt + UNROLL <= nk; kt += UNROLL) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) KD_SLICE(u, kt + u);
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL - 1; ++u)
+    if (kt + u < nk) KD_SLICE(u, kt + u);
+#undef KD_A
+#undef KD_B
+#undef KD_LOADA
+#undef KD_LOADB
+#undef KD_READ
+#undef KD_FENCE
+#undef KD_MMA
+#undef KD_STEP0
+#undef KD_STEP1
+#undef KD_SLICE
+  __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00);  // vmcnt(0): no load still writes the stages
+  // the MFMAs are assembly, so the compiler inserts no wait states between the last of them and the first read of
+  // their results: 24 cycles cover the longest 16x16 form
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __syncthreads();  // every wave is done with the stages before their LDS becomes the store patches
+  uint32_t* patch = reinterpret_cast<uint32_t*>(la0) + wave * PATCH_WORDS;
+  store_tile16<false, 4, 4, Acc32>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
 }
 
 // Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
@@ -1532,8 +1861,21 @@ static int launch_quad(const void* a, const void* b, void* c, int64_t m, int64_t
     krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
     return -1;
   }
-  hipLaunchKernelGGL((gemm_quad<FMT>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
-                     (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+#ifndef KRN_DTL16
+#define KRN_DTL16 1
+#endif
+  if constexpr (KRN_DTL16 && (FMT == FMT_BF16 || FMT == FMT_F16))
+#ifndef KRN_D16_NA
+#define KRN_D16_NA 2
+#endif
+#ifndef KRN_D16_NB
+#define KRN_D16_NB 3
+#endif
+    hipLaunchKernelGGL((gemm_dtl16<FMT, KRN_D16_NA, KRN_D16_NB>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
+                       (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  else
+    hipLaunchKernelGGL((gemm_quad<FMT>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
+                       (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     krn_set_error("gemm launch: %s", hipGetErrorString(err));
