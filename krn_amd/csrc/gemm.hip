@@ -102,9 +102,9 @@ struct Mfma<FMT_FP8> {
 
 // The 16x16 forms, which consume twice the K per instruction for 16-bit and int8 operands. On gfx950 they sustain
 // more throughput than the 32x32 forms under the same power limit (MFMA-only loops on random operands: bf16
-// 16x16x32 0.93 of the per-clock peak at 1.71 GHz against 0.84 at 1.62 GHz for 32x32x16; int8 16x16x64 0.95 at
-// 1.79 GHz against 0.85 at 1.59 GHz). Operand lane L holds row (or column) L & 15 and 16 bytes of K from
-// (L >> 4) * 16; accumulator lane L holds column L & 15 of rows 4 (L >> 4) .. + 3.
+// 16x16x32 0.93 of the per-clock peak at 1.71 GHz against 0.84 at 1.62 GHz for 32x32x16). Operand lane L holds row
+// (or column) L & 15 and 16 bytes of K from (L >> 4) * 16; accumulator lane L holds column L & 15 of rows
+// 4 (L >> 4) .. + 3.
 template <int FMT>
 struct Mfma16;
 
@@ -134,24 +134,6 @@ struct Mfma16<FMT_F16> {
   }
 };
 
-template <>
-struct Mfma16<FMT_I8> {
-  typedef i32x4 Acc;
-  __device__ static void step(Acc& c, u32x4 a, u32x4 b) {
-    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0,
-                                              0);
-  }
-  __device__ static void step_agpr(Acc& c, u32x4 a, u32x4 b) {
-    asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-  }
-};
-
-// Four 16x16 accumulator blocks s[R][C] (rows 16 R, columns 16 C of a 32 x 32 block) in the layout of one 32x32
-// accumulator, so that every store path serves both forms. Target lane L = (h5, h4, low4) register
-// 8 R + 4 b + q holds row 8 (2 R + b) + 4 h5 + q, column 16 h4 + low4: that is register q of block s[R][h4] at lane
-// (b, h5, low4). Per pair of source registers (the same q of s[R][0] and s[R][1], as 16-lane rows [a0 a1 a2 a3] and
-// [b0 b1 b2 b3]) a v_permlane16_swap gives [a0 b0 a2 b2] and [a1 b1 a3 b3], and a v_permlane32_swap of those gives
-// [a0 b0 a1 b1] (b = 0) and [a2 b2 a3 b3] (b = 1).
 template <typename V>
 struct Elem;
 template <>
@@ -1312,7 +1294,7 @@ __global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ 
 // have landed; after it the loads of slice kt + N of an operand with N stages go into the stage slice kt leaves,
 // and the fragments of slice kt + 1 are read as step 1 frees their registers. An operand's slice thus has N - 1
 // slices of MFMA time to arrive.
-template <int FMT, int NA = 2, int NB = 2>
+template <int FMT, int NA = 2, int NB = 2, bool NN = false>
 __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
                                                      void* __restrict__ C, int64_t M, int64_t N, int64_t kbytes,
                                                      int64_t lda, int64_t ldb, int64_t ldc, Epilogue e) {
@@ -1320,6 +1302,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
   typedef Mfma16<FMT> Unit;
   typedef typename Unit::Acc Acc;
   typedef typename Mfma<FMT>::Acc Acc32;
+  static_assert(FMT == FMT_BF16 || FMT == FMT_F16, "16-bit operands");
   constexpr int BM = 256, BN = 256, BKB = 128;
   constexpr int HALF = BM * BKB;  // 32 KiB: one operand's rows of one slice
   constexpr int UNROLL = NA == NB ? 2 : 6;  // slices per loop iteration: every stage index a constant
@@ -1341,19 +1324,39 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
     return (const void*)(((uint64_t)hi << 32) | lo);
   };
   const int64_t a_bytes = __builtin_amdgcn_readfirstlane((int)min((M - m0) * lda, (int64_t)0x7fffffff));
-  const int64_t b_bytes = __builtin_amdgcn_readfirstlane((int)min((N - n0) * ldb, (int64_t)0x7fffffff));
+  // NN: the panel is columns n0 .. n0 + 255 of every row of B (the host checks that it is addressable)
+  const int64_t b_bytes = __builtin_amdgcn_readfirstlane(
+      NN ? (int)((kbytes / 2 - 1) * ldb + BN * 2) : (int)min((N - n0) * ldb, (int64_t)0x7fffffff));
   const __amdgpu_buffer_rsrc_t a_rsrc = panel_rsrc(uniform(A + m0 * lda), a_bytes),
-                              b_rsrc = panel_rsrc(uniform(B + n0 * ldb), b_bytes);
+                              b_rsrc = panel_rsrc(uniform(B + (NN ? n0 * 2 : n0 * ldb)), b_bytes);
   // load item j of an operand: rows 64 wave + 8 j .. + 7; lane i takes row i / 8 and the global chunk that belongs at
   // slot i % 8. The swizzle of row 8 j + i / 8 depends on j only through j & 1.
   const int lrow = lane >> 3, lslot = lane & 7;
-  uint32_t ga[2], gb[2];
+  uint32_t ga[2], gb[4];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const int row = wave * 64 + p * 8 + lrow;
     ga[p] = (uint32_t)(row * lda + ((lslot ^ swz8(row)) * 16));
     gb[p] = (uint32_t)(row * ldb + ((lslot ^ swz8(row)) * 16));
   }
+  // NN: a slice of B is 64 k rows of 512 bytes ([k][n]); wave w loads k rows 16 w .. 16 w + 15, two per load (item
+  // j: rows 16 w + 2 j + i / 32, lane i at slot i % 32). Chunk c of row k sits at slot c ^ nn_swz(k), which puts the
+  // 8 rows a transposed fragment read serves per pass on 8 distinct 32-byte bank groups. The lane offsets depend on
+  // j through j & 1 and j >> 2; the rest is the scalar offset 2 j ldb.
+  auto nn_swz = [](int k) { return 2 * ((k & 3) | (((k >> 3) & 1) << 2)); };
+  if constexpr (NN) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = (q >> 1) * 4 + (q & 1);
+      const int krow = wave * 16 + 2 * j + (lane >> 5), slot = lane & 31;
+      gb[q] = (uint32_t)((wave * 16 + (lane >> 5)) * ldb + ((slot ^ nn_swz(krow)) * 16));
+    }
+  }
+  // NN fragment reads (ds_read_b64_tr_b16): lane L = 16 g + a reads k row 8 g + 4 p + a / 4 (part p) of the step's
+  // 32 and columns 4 (a % 4) .. + 3 of its 16, and receives column a of the 16 at the four k of the part
+  const int tg = lane >> 4, ta = lane & 15;
+  const int tr_row = (8 * tg + (ta >> 2)) * 512, tr_swz = nn_swz(8 * tg + (ta >> 2));
+  const int tr_col = wn * 128 + 4 * (ta & 3);
   const int wbase = wave * 8192;
   // fragment bases: lane L reads row L & 15 of a 16-row half, 16-byte chunk 4 s + (L >> 4) (step s)
   int ra[2], rb[2];
@@ -1377,42 +1380,49 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
 #define KD_LOADA(j, sl, pa)                                                                                    \
   buffer_to_lds16(a_rsrc, KD_A(pa) + wbase + (j) * 1024, ga[(j) & 1], (int)((sl) * BKB + ((j) & 6) * 8 * lda))
 #define KD_LOADB(j, sl, pb)                                                                                    \
-  buffer_to_lds16(b_rsrc, KD_B(pb) + wbase + (j) * 1024, gb[(j) & 1], (int)((sl) * BKB + ((j) & 6) * 8 * ldb))
-#define KD_READ(r, c, pa, pb, s)                                                                               \
-  F[(r) * 2 + (c)] = *reinterpret_cast<const u32x4*>(                                                          \
-      ((r) < 4 ? KD_A(pa) + ra[s] : KD_B(pb) + rb[s]) + (((r) & 3) * 32 + (c) * 16) * 128)
-#define KD_FENCE() __builtin_amdgcn_sched_barrier(0)
-#define KD_MMA(m)                                                                                              \
-  _Pragma("unroll") for (int R = 0; R < 2; ++R) _Pragma("unroll") for (int Q = 0; Q < 2; ++Q)                 \
-      Unit::step_agpr(acc[((m) >> 2) * 2 + R][((m) & 3) * 2 + Q], F[((m) >> 2) * 2 + R], F[8 + ((m) & 3) * 2 + Q])
-  // step 0 of slice kt (A stage PA, B stage PB): its groups row by row; the step-1 fragments as registers free up
-#define KD_STEP0(PA, PB)                                                                                       \
   do {                                                                                                         \
-    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
-      KD_MMA(m);                                                                                               \
-      KD_FENCE();                                                                                              \
-      if ((m & 3) == 3) {                                                                                      \
-        KD_READ(m >> 2, 0, PA, PB, 1);                                                                         \
-        KD_READ(m >> 2, 1, PA, PB, 1);                                                                         \
-        KD_FENCE();                                                                                            \
-      }                                                                                                        \
-      if ((m >> 2) == 3) {                                                                                     \
-        KD_READ(4 + (m & 3), 0, PA, PB, 1);                                                                    \
-        KD_READ(4 + (m & 3), 1, PA, PB, 1);                                                                    \
-        KD_FENCE();                                                                                            \
-      }                                                                                                        \
+    if constexpr (NN)                                                                                          \
+      buffer_to_lds16(b_rsrc, KD_B(pb) + wbase + (j) * 1024, gb[((j) >> 2) * 2 + ((j) & 1)],                   \
+                      (int)(((sl) * 64 + 2 * (j)) * ldb));                                                     \
+    else                                                                                                       \
+      buffer_to_lds16(b_rsrc, KD_B(pb) + wbase + (j) * 1024, gb[(j) & 1],                                      \
+                      (int)((sl) * BKB + ((j) & 6) * 8 * ldb));                                                \
+  } while (0)
+#define KD_TR(pb, s, p, col)                                                                                   \
+  __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s16*)( \
+                                KD_B(pb) + tr_row + ((s) * 32 + (p) * 4) * 512 +                               \
+                                ((((col) >> 3) ^ tr_swz) * 16) + ((col) & 7) * 2)))
+#define KD_READ(r, c, pa, pb, s)                                                                               \
+  do {                                                                                                         \
+    if (NN && (r) >= 4) {                                                                                      \
+      const int col = tr_col + ((r) - 4) * 32 + (c) * 16;                                                      \
+      const u32x2 lo = KD_TR(pb, s, 0, col), hi = KD_TR(pb, s, 1, col);                                        \
+      F[(r) * 2 + (c)] = u32x4{lo[0], lo[1], hi[0], hi[1]};                                                    \
+    } else {                                                                                                   \
+      F[(r) * 2 + (c)] = *reinterpret_cast<const u32x4*>(                                                      \
+          ((r) < 4 ? KD_A(pa) + ra[s] : KD_B(pb) + rb[s]) + (((r) & 3) * 32 + (c) * 16) * 128);                \
     }                                                                                                          \
   } while (0)
-  // step 1 of slice kt: column by column. After group 3 the barrier (this wave's loads of slice kt + 1 landed: only
-  // the loads of a three-stage operand's slice kt + 2, issued last, may still be in flight), then the loads into the
-  // stages slice kt leaves, two-stage operands first (past the end: the last slice again, into a stage nothing
-  // reads any more), and the step-0 fragments of slice kt + 1
-#define KD_STEP1(PA, PB, kt)                                                                                   \
+#define KD_FENCE() __builtin_amdgcn_sched_barrier(0)
+#define KD_MMA(I, J)                                                                                           \
+  _Pragma("unroll") for (int R = 0; R < 2; ++R) _Pragma("unroll") for (int Q = 0; Q < 2; ++Q)                 \
+      Unit::step_agpr(acc[(I) * 2 + R][(J) * 2 + Q], F[(I) * 2 + R], F[8 + (J) * 2 + Q])
+  // One step of slice kt (A stage PA, B stage PB). ORD 0: its 16 blocks row by row (group g = 4 I + J), 1: column
+  // by column (g = 4 J + I); either way A block I is dead after its group with J = 3 and B block J after its group
+  // with I = 3, and the next step's fragments of that block are read at once (ORD 0 reads A first, 1 reads B first).
+  // The next step is step s + 1 of this slice, or (LAST) step 0 of slice kt + 1. In the last step, after group 3,
+  // the barrier (this wave's loads of slice kt + 1 landed: only the loads of a three-stage operand's slice kt + 2,
+  // issued last, may still be in flight), then the loads into the stages slice kt leaves, two-stage operands first
+  // (past the end: the last slice again, into a stage nothing reads any more).
+#define KD_STEP(PA, PB, ORD, LAST, kt, s)                                                                      \
   do {                                                                                                         \
+    const int NA_ = (LAST) ? ((PA) + 1) % NA : (PA), NB_ = (LAST) ? ((PB) + 1) % NB : (PB);                    \
+    const int NS_ = (LAST) ? 0 : (s) + 1;                                                                      \
     _Pragma("unroll") for (int g = 0; g < 16; ++g) {                                                           \
-      KD_MMA((g & 3) * 4 + (g >> 2));                                                                          \
+      const int I = (ORD) ? (g & 3) : (g >> 2), J = (ORD) ? (g >> 2) : (g & 3);                                \
+      KD_MMA(I, J);                                                                                            \
       KD_FENCE();                                                                                              \
-      if (g == 3) {                                                                                            \
+      if ((LAST) && g == 3) {                                                                                  \
         if constexpr (NA == 3 || NB == 3)                                                                      \
           __builtin_amdgcn_s_waitcnt(0x0070 | 8); /* vmcnt(8) lgkmcnt(0) */                                     \
         else                                                                                                   \
@@ -1420,43 +1430,36 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
         __builtin_amdgcn_s_barrier();                                                                          \
         KD_FENCE();                                                                                            \
       }                                                                                                        \
-      if (!KRN_D16_NOLOAD && g >= 3 && g < 11) {                                                               \
+      if ((LAST) && !KRN_D16_NOLOAD && g >= 3 && g < 11) {                                                     \
         const int j = 2 * (g - 3);                                                                             \
-        if (j < 8) {                                                                                           \
-          if constexpr (NB <= NA) {                                                                            \
-            KD_LOADB(j, min((kt) + NB, nk - 1), PB);                                                       \
-            KD_LOADB(j + 1, min((kt) + NB, nk - 1), PB);                                                   \
-          } else {                                                                                             \
-            KD_LOADA(j, min((kt) + NA, nk - 1), PA);                                                       \
-            KD_LOADA(j + 1, min((kt) + NA, nk - 1), PA);                                                   \
-          }                                                                                                    \
+        if ((j < 8) == (NB <= NA)) {                                                                           \
+          KD_LOADB(j & 7, min((kt) + NB, nk - 1), PB);                                                         \
+          KD_LOADB((j & 7) + 1, min((kt) + NB, nk - 1), PB);                                                   \
         } else {                                                                                               \
-          if constexpr (NB <= NA) {                                                                            \
-            KD_LOADA(j - 8, min((kt) + NA, nk - 1), PA);                                                   \
-            KD_LOADA(j - 7, min((kt) + NA, nk - 1), PA);                                                   \
-          } else {                                                                                             \
-            KD_LOADB(j - 8, min((kt) + NB, nk - 1), PB);                                                   \
-            KD_LOADB(j - 7, min((kt) + NB, nk - 1), PB);                                                   \
-          }                                                                                                    \
+          KD_LOADA(j & 7, min((kt) + NA, nk - 1), PA);                                                         \
+          KD_LOADA((j & 7) + 1, min((kt) + NA, nk - 1), PA);                                                   \
         }                                                                                                      \
         KD_FENCE();                                                                                            \
       }                                                                                                        \
-      if ((g & 3) == 3) {                                                                                      \
-        KD_READ(4 + (g >> 2), 0, ((PA) + 1) % NA, ((PB) + 1) % NB, 0);                                          \
-        KD_READ(4 + (g >> 2), 1, ((PA) + 1) % NA, ((PB) + 1) % NB, 0);                                          \
-        KD_FENCE();                                                                                            \
-      }                                                                                                        \
-      if ((g >> 2) == 3) {                                                                                     \
-        KD_READ(g & 3, 0, ((PA) + 1) % NA, ((PB) + 1) % NB, 0);                                                 \
-        KD_READ(g & 3, 1, ((PA) + 1) % NA, ((PB) + 1) % NB, 0);                                                 \
-        KD_FENCE();                                                                                            \
+      _Pragma("unroll") for (int o = 0; o < 2; ++o) {                                                          \
+        if ((o == 0) == ((ORD) == 0) && J == 3) {                                                              \
+          KD_READ(I, 0, NA_, NB_, NS_);                                                                        \
+          KD_READ(I, 1, NA_, NB_, NS_);                                                                        \
+          KD_FENCE();                                                                                          \
+        }                                                                                                      \
+        if ((o == 0) == ((ORD) == 1) && I == 3) {                                                              \
+          KD_READ(4 + J, 0, NA_, NB_, NS_);                                                                    \
+          KD_READ(4 + J, 1, NA_, NB_, NS_);                                                                    \
+          KD_FENCE();                                                                                          \
+        }                                                                                                      \
       }                                                                                                        \
     }                                                                                                          \
   } while (0)
+  // slice u of an unrolled run: step 0 row by row, step 1 column by column
 #define KD_SLICE(u, kt)                                                                                        \
   do {                                                                                                         \
-    KD_STEP0((u) % NA, (u) % NB);                                                                              \
-    KD_STEP1((u) % NA, (u) % NB, kt);                                                                          \
+    KD_STEP((u) % NA, (u) % NB, 0, false, kt, 0);                                                              \
+    KD_STEP((u) % NA, (u) % NB, 1, true, kt, 1);                                                               \
   } while (0)
 
   // the prologue: the first NA slices of A and NB of B, slice by slice (a three-stage operand's third slice last,
@@ -1508,9 +1511,9 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
 #undef KD_READ
 #undef KD_FENCE
 #undef KD_MMA
-#undef KD_STEP0
-#undef KD_STEP1
+#undef KD_STEP
 #undef KD_SLICE
+#undef KD_TR
   __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00);  // vmcnt(0): no load still writes the stages
   // the MFMAs are assembly, so the compiler inserts no wait states between the last of them and the first read of
   // their results: 24 cycles cover the longest 16x16 form
@@ -1861,21 +1864,32 @@ static int launch_quad(const void* a, const void* b, void* c, int64_t m, int64_t
     krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
     return -1;
   }
-#ifndef KRN_DTL16
-#define KRN_DTL16 1
-#endif
-  if constexpr (KRN_DTL16 && (FMT == FMT_BF16 || FMT == FMT_F16))
+  hipLaunchKernelGGL((gemm_quad<FMT>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
+                     (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    krn_set_error("gemm launch: %s", hipGetErrorString(err));
+    return (int)err;
+  }
+  return 0;
+}
+
 #ifndef KRN_D16_NA
 #define KRN_D16_NA 2
 #endif
 #ifndef KRN_D16_NB
 #define KRN_D16_NB 3
 #endif
-    hipLaunchKernelGGL((gemm_dtl16<FMT, KRN_D16_NA, KRN_D16_NB>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
-                       (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
-  else
-    hipLaunchKernelGGL((gemm_quad<FMT>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
-                       (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
+template <int FMT>
+static int launch_dtl16(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                        int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+  const int64_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
+  if (tiles > 0x7fffffff) {
+    krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
+    return -1;
+  }
+  hipLaunchKernelGGL((gemm_dtl16<FMT, KRN_D16_NA, KRN_D16_NB>), dim3((unsigned)tiles), dim3(256), 0, stream,
+                     (const uint8_t*)a, (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     krn_set_error("gemm launch: %s", hipGetErrorString(err));
@@ -1965,17 +1979,20 @@ static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64
 template <int FMT>
 static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  // bf16/f16 and fp8: four waves of 128 x 128 in a fixed instruction order (fp8 8192^3 7 % faster than the
-  // eight-wave ping-pong, which keeps the one-slice K = 128 case). int8: eight waves (4 x 2, each 64 x 128 of the
-  // tile) that interleave their own LDS reads with their MFMAs (the four-wave loop measured 7-10 % slower on W8A8
-  // M = 4096, whose K of 32 slices leaves more of the time to the prologue and epilogue).
+  // bf16/f16: four waves of 128 x 128 on 16x16x32 MFMAs with direct-to-LDS slices (8192^3 1424 TFLOP/s against
+  // 1335 for the register-staged 32x32 loop). fp8: the register-staged four-wave loop on 32x32x64 MFMAs (7 % faster
+  // than the eight-wave ping-pong, which keeps the one-slice K = 128 case); the direct-to-LDS loop on 16x16x128 ran
+  // at a higher clock with proportionally less MFMA time, equal overall. int8: eight waves (4 x 2, each 64 x 128 of
+  // the tile) that interleave their own LDS reads with their MFMAs (the four-wave register-staged loop 7-10 % and
+  // the direct-to-LDS 16x16x64 loop 2 % slower on W8A8 M = 4096, whose K of 32 slices leaves more of the time to
+  // the prologue and epilogue).
   if constexpr (FMT == FMT_FP8) {
     if (kbytes >= 256) return launch_quad<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
     return launch_pp<FMT, 4>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   } else if constexpr (FMT == FMT_I8) {
     return launch_pipe<FMT, 256, 256, 4, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   } else {
-    if (kbytes % 128 == 0 && kbytes >= 256) return launch_quad<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    if (kbytes % 128 == 0 && kbytes >= 256) return launch_dtl16<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
     return launch_pipe<FMT, 256, 256, 4, 2, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   }
 }
@@ -2176,7 +2193,18 @@ static int gemm_nn_through(int in_kind, const void* a, const void* b, void* c, i
       return -1;
     }
     const int64_t tiles = ((m + 255) / 256) * (n / 256);
-    if (in_kind == BF16)
+#ifndef KRN_NN_DTL
+#define KRN_NN_DTL 1
+#endif
+    if (KRN_NN_DTL && in_kind == BF16)
+      hipLaunchKernelGGL((gemm_dtl16<FMT_BF16, KRN_D16_NA, KRN_D16_NB, true>), dim3((unsigned)tiles), dim3(256), 0,
+                         (hipStream_t)stream, (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n,
+                         e);
+    else if (KRN_NN_DTL)
+      hipLaunchKernelGGL((gemm_dtl16<FMT_F16, KRN_D16_NA, KRN_D16_NB, true>), dim3((unsigned)tiles), dim3(256), 0,
+                         (hipStream_t)stream, (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n,
+                         e);
+    else if (in_kind == BF16)
       hipLaunchKernelGGL((gemm_quad<FMT_BF16, true>), dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
                          (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n, e);
     else
