@@ -3,11 +3,12 @@
 // This is the lowering of krn's tile contraction `acc += a[rows, ks] @ b[cols, ks].transpose()` followed by
 // `c[rows, cols] = f(acc).to(dtype)` (reference compiler/ir.py:309-315 Accumulate, compiler/emit.py:788-821). One
 // workgroup owns a BM x BN output tile split among its waves, and every wave keeps its accumulators in registers as
-// 32x32 MFMA blocks. Main loops: `gemm_quad` (bf16/f16/fp8, also the NN form), `gemm_pipe` (int8) and `gemm_pp`
-// (fp8 with one slice) for whole 256 x 256 tiles (see each; `gemm_pipe` also on 128 x 128 and 128 x 256 tiles for
-// mid-size products), `gemm_skinny` for M <= 128 (rings of direct-to-LDS slices per wave), and `gemm_tile` for the
-// rest (128-byte slices staged through registers, bounds-checked, double buffered). All end in `store_tile`: whole
-// blocks straight from the accumulators (the direct epilogue), the rest through an LDS patch.
+// 32x32 MFMA blocks (or four 16x16 blocks joined into that layout when stored). Main loops: `gemm_quad16` (every
+// format, also the bf16/f16 NN form, 16x16 MFMAs) for whole 256 x 256 tiles of two K slices or more, `gemm_pipe`
+// and `gemm_pp` (fp8) for one slice and, `gemm_pipe`, on 128 x 128 and 128 x 256 tiles for mid-size products,
+// `gemm_skinny` for M <= 128 (rings of direct-to-LDS slices per wave), and `gemm_tile` for the rest (128-byte
+// slices staged through registers, bounds-checked, double buffered). All end in `store_tile`: whole blocks straight
+// from the accumulators (the direct epilogue), the rest through an LDS patch.
 //
 // One byte-oriented main loop serves three operand formats, because each MFMA consumes the same 16 bytes per lane
 // per half-wave:
@@ -131,6 +132,25 @@ struct Mfma16<FMT_F16> {
   }
   __device__ static void step_agpr(Acc& c, u32x4 a, u32x4 b) {
     asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+};
+
+template <>
+struct Mfma16<FMT_I8> {
+  typedef i32x4 Acc;
+  __device__ static void step_agpr(Acc& c, u32x4 a, u32x4 b) {
+    asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+};
+
+template <>
+struct Mfma16<FMT_FP8> {
+  typedef f32x4 Acc;
+  // v_mfma_scale_f32_16x16x128_f8f6f4 on e4m3 operands (format 0) with unit E8M0 scales (127 = 2^0, in `one`)
+  __device__ static void step_agpr(Acc& c, i32x8 a, i32x8 b, int one) {
+    asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0]"
+                 : "+a"(c)
+                 : "v"(a), "v"(b), "v"(one));
   }
 };
 
@@ -624,8 +644,9 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int& tm, int& 
 #ifndef KRN_XCD_REMAP
 #define KRN_XCD_REMAP 1
 #endif
-  constexpr int GROUP_M = KRN_GROUP_M;  // bf16 8192^3: 0.5-1.5 % faster than 8 (2: -6 %, 6: -1 %, 16: -9 %); fp8
-                                        // equal; the four-wave loop: 8 equal, 2 -1.5 %
+  constexpr int GROUP_M = KRN_GROUP_M;  // bf16 8192^3, eight-wave ring: 0.5-1.5 % faster than 8 (2: -6 %, 6: -1 %,
+                                        // 16: -9 %); fp8 equal; four-wave register-staged 32x32 loop: 8 equal, 2
+                                        // -1.5 % (1.5 times the bytes read)
   int nb = tiles_m * tiles_n;
   int bid = blockIdx.x;
   if (KRN_XCD_REMAP && nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
@@ -991,327 +1012,50 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
   store_tile<FMT == FMT_I8>(acc, patch, C, ldc, m0 + wm * (BM / WM), n0 + wn * (BN / WN), M, N, e, lane);
 }
 
-// Four-wave main loop for whole 256 x 256 bf16/f16/fp8 tiles with K a multiple of 128 bytes. Each wave owns a 128 x 128
-// quarter (wave w: rows 128 (w >> 1), columns 128 (w & 1)), 16 accumulator blocks in AGPRs, one wave per SIMD.
-// 128-byte K slices go global -> registers -> LDS: while slice kt multiplies, slice kt + 1 is written from registers
-// into the other of two LDS stages and its registers are reloaded with slice kt + 3 (bf16/f16: two register sets,
-// so a slice has two slices of MFMA time to arrive; fp8, whose fragments take twice the registers: one set, slice
-// kt + 2); the same 16 loads and 16 writes per wave and slice as hipBLASLt's kernel makes. Every instruction of a slice has a fixed place (sched_barrier): per
-// MFMA step 16 MFMAs, each followed by at most one LDS read of the next step's fragments, one LDS write and one
-// global load, so the matrix core is never left waiting behind a burst of memory instructions; the one barrier per
-// slice comes after the eighth MFMA of the last step, once this wave's writes of slice kt + 1 have landed, and the
-// first fragments of slice kt + 1 are read in the shadow of the last eight MFMAs. Past the end the loads re-read the
-// last slice and the writes go to the stage that is not read again, so every slice runs the same code.
-// bf16 8192^3: with one register set 3-5 % faster than the eight-wave ring with direct-to-LDS slices, whose loads
-// cost about a sixth of its loop in LDS bandwidth (eight waves of 64 x 128 read 96 KiB of fragments per 64-byte
-// slice, four of 128 x 128 read 64 KiB per 128-byte slice); the second set another 6 %. fp8 8192^3: 7 % faster than
-// the eight-wave ping-pong.
+// The four-wave main loop for whole 256 x 256 tiles with K a multiple of 128 bytes (bf16/f16 NT and NN, fp8, int8),
+// on the 16x16 MFMA forms. Each wave owns a 128 x 128 quarter (wave w: rows 128 (w >> 1), columns 128 (w & 1)) as
+// 8 x 8 accumulator blocks of 16 x 16 in AGPRs. 128-byte K slices go straight from global memory into LDS stages,
+// two for A and three for B (5 x 32 KiB fill the 160 KiB), each stage a separate array so that the compiler can tell
+// every fragment read from the loads in flight into the other stages; wave w loads rows 64 w .. 64 w + 63 of A and
+// of B, 8 rows (1 KiB) per load, chunk c of row r at slot c ^ ((r >> 1) & 7).
 //
-// NN: B is stored K x N (row k of B is `ldb` bytes apart, N a multiple of 256, 16-bit elements): a slice of B is 64
-// rows of 512 bytes kept in LDS as [k][n] with 16-byte chunk c of row k at slot c ^ 4 (k & 3), and every B fragment
-// is two transposed reads (ds_read_b64_tr_b16) that hand lane L column n = L & 31 of its block and the same eight
-// k as the lane's A fragment holds. No transposed copy of B is made.
+// bf16/f16/int8: a slice is two steps of 64 bytes of K; fp8: one step of 128 (16x16x128). One set of fragments (A
+// blocks 0-3 and B blocks 0-3 of 32 rows, each two 16-row halves) is refilled in place: steps alternate between
+// running their 16 blocks of 32 x 32 row by row (block (I, J) is group 4 I + J of four MFMAs) and column by column,
+// so a block's fragments are dead after its last group of the step and take the next step's at once (row order
+// frees A block I after group 4 I + 3 and B block J after 12 + J; column order frees B block J after 4 J + 3 and A
+// block I after 12 + I). The one barrier per slice sits after group 3 of its last step: by then this wave has read
+// all of slice kt and its loads of slice kt + 1 have landed. B's slice kt + 2 is loaded during the slice, before
+// and after the barrier (into the stage slice kt - 1 left, free since the last barrier), one load every other group;
+// A's slice kt + 2 after the barrier, one load per group, into the stage slice kt leaves. Loads issued in a burst
+// (the 16 of a slice in 8 groups) ask the vector memory path for twice what it delivers and stall the MFMA issue
+// behind them (bf16 8192^3: 1452 TFLOP/s spread against 1392, MFMA busy 0.79 against 0.71; 0.84 with no loads).
+//
+// Measured against the 32x32 forms: MFMA-only loops on random operands sustain 16 % (bf16) and 25 % (int8) more
+// on 16x16 at the same power limit; bf16 8192^3 on the register-staged 32x32 loop 1335 TFLOP/s, W8A8 M = 4096 on
+// the eight-wave 32x32 loop 0.275 ms against 0.269; fp8 8192^3 equal (0.442 ms), the 16x16 form at a higher clock
+// with proportionally less MFMA time.
 template <int FMT, bool NN = false>
-__global__ __launch_bounds__(256, 1) void gemm_quad(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
-                                                    void* __restrict__ C, int64_t M, int64_t N, int64_t kbytes,
-                                                    int64_t lda, int64_t ldb, int64_t ldc, Epilogue e) {
-  typedef Mfma<FMT> Unit;
-  typedef typename Unit::Acc Acc;
-  constexpr int BM = 256, BN = 256, BKB = 128;
-  constexpr int CH = Unit::kBytes / 32;  // 16-byte chunks per lane and operand of one MFMA (bf16/f16/int8 1, fp8 2)
-  constexpr int NS = BKB / Unit::kBytes; // MFMA steps per slice (4 or 2)
-  static_assert(CH == 1 || CH == 2, "32 or 64 bytes of K per MFMA");
-  constexpr int STAGE = (BM + BN) * BKB;  // 64 KiB: A rows, then B rows, 128 bytes each, chunks swizzled by swz8
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE];
-  int tm, tn;
-  tile_of((int)((M + BM - 1) / BM), (int)((N + BN - 1) / BN), tm, tn);
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int half = lane >> 5, r32 = lane & 31;
-  // The buffer resources must be visibly wave-uniform, or every load is wrapped in a readfirstlane loop.
-  auto uniform = [](const void* p) {
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (const void*)(((uint64_t)hi << 32) | lo);
-  };
-  const int64_t a_bytes = __builtin_amdgcn_readfirstlane((int)min((M - m0) * lda, (int64_t)0x7fffffff));
-  static_assert(!NN || CH == 1, "NN: 16-bit operands");
-  // NN: the panel is columns n0 .. n0 + 255 of every row of B (the host checks that it is addressable)
-  const int64_t b_bytes = __builtin_amdgcn_readfirstlane(
-      NN ? (int)((kbytes / 2 - 1) * ldb + BN * 2) : (int)min((N - n0) * ldb, (int64_t)0x7fffffff));
-  const __amdgpu_buffer_rsrc_t a_rsrc = panel_rsrc(uniform(A + m0 * lda), a_bytes),
-                              b_rsrc = panel_rsrc(uniform(B + (NN ? n0 * 2 : n0 * ldb)), b_bytes);
-  // wave w stages rows 64 w .. 64 w + 63 of A and of B, 8 rows (1 KiB) per load; lane i takes row i / 8 and the
-  // global chunk that belongs at slot i % 8
-  const int lrow = lane >> 3, lslot = lane & 7;
-  uint32_t ga[8], gb[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = wave * 64 + j * 8 + lrow;
-    ga[j] = (uint32_t)(row * lda + ((lslot ^ swz8(row)) * 16));
-    gb[j] = (uint32_t)(row * ldb + ((lslot ^ swz8(row)) * 16));
-    if constexpr (NN) {
-      // wave w stages k rows 16 w .. 16 w + 15 of the slice, two 512-byte rows per load; lane i takes row i / 32 and
-      // the chunk that belongs at slot i % 32
-      const int krow = wave * 16 + j * 2 + (lane >> 5), slot = lane & 31;
-      gb[j] = (uint32_t)(krow * ldb + ((slot ^ (4 * (krow & 3))) * 16));
-    }
-  }
-  // NN: per lane, the byte offset in a stage's B part of its transposed reads for block j at step 0 (the key rows
-  // (g / 2) 8 + (a16 / 4) and + 4, columns 32 j + (g % 2) 16 + 4 (a16 % 4) of this wave's 128, g = lane / 16)
-  int trb[4] = {0, 0, 0, 0};
-  if constexpr (NN) {
-    const int g = lane >> 4, a16 = lane & 15;
-    const int krow = (g >> 1) * 8 + (a16 >> 2);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = wn * 128 + j * 32 + (g & 1) * 16 + 4 * (a16 & 3);
-      trb[j] = krow * 512 + (((n >> 3) ^ (4 * (krow & 3))) * 16) + (n & 7) * 2;
-    }
-  }
-  const int b_step = NN ? 64 * (int)ldb : BKB;  // bytes from one slice of B to the next
-  // fragment of MFMA step s: chunks (2 s + half) CH + c of row r32 of a 32-row block (the swizzle depends on r32 only)
-  const int sw = (r32 >> 1) & 7;
-  int rd[NS][CH];
-#pragma unroll
-  for (int s = 0; s < NS; ++s)
-#pragma unroll
-    for (int c = 0; c < CH; ++c) rd[s][c] = r32 * 128 + ((((2 * s + half) * CH + c) ^ sw) * 16);
-  const int wr = wave * 8192 + lane * 16;
-  const int nk = (int)(kbytes / BKB);  // >= 2 (host)
-  // register sets of one slice of this wave's rows each (0-7 A, 8-15 B): with two, a slice is loaded two slices
-  // before it is written to LDS, which covers an L2 miss under load (about 3000 cycles against 2048 per slice);
-  // fp8's fragments take the registers of a second set
-  constexpr int NSET = CH == 1 ? 2 : 1;
-  u32x4 stg[NSET][16];
-  u32x4 F0[8 * CH], F1[8 * CH];  // fragments of two MFMA steps: 0-3 the A blocks, 4-7 the B blocks, CH chunks each
-  Acc acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = Acc{};
-
-#define KQ_LOAD(q, slice)                                                                                      \
-  do {                                                                                                         \
-    if ((q) < 8)                                                                                               \
-      stg[SET_][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ga[(q) & 7], (slice) * BKB, 0)); \
-    else                                                                                                       \
-      stg[SET_][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, gb[(q) & 7], (slice) * b_step, 0)); \
-  } while (0)
-#define KQ_WRITE(q, slice)                                                                                     \
-  *reinterpret_cast<u32x4*>(lds + ((slice) & 1) * STAGE + ((q) < 8 ? 0 : BM * BKB) + wr + ((q) & 7) * 1024) = stg[SET_][q]
-#define KQ_READC(F, r, c, slice, s)                                                                            \
-  do {                                                                                                         \
-    if (NN && (r) >= 4) {                                                                                      \
-      const uint8_t* p = lds + ((slice) & 1) * STAGE + BM * BKB + trb[((r) - 4) & 3] + (s) * 16 * 512;          \
-      const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(                        \
-                        (__attribute__((address_space(3))) v4s16*)p));                                          \
-      const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(                        \
-                        (__attribute__((address_space(3))) v4s16*)(p + 4 * 512)));                              \
-      F[(r) * CH + (c)] = u32x4{lo[0], lo[1], hi[0], hi[1]};                                                   \
-    } else {                                                                                                   \
-      F[(r) * CH + (c)] = *reinterpret_cast<const u32x4*>(                                                     \
-          lds + ((slice) & 1) * STAGE + rd[s][c] +                                                             \
-          ((r) < 4 ? (wm * 128 + (r) * 32) * 128 : BM * BKB + (wn * 128 + ((r) - 4) * 32) * 128));             \
-    }                                                                                                          \
-  } while (0)
-#define KQ_FENCE() __builtin_amdgcn_sched_barrier(0)
-#define KQ_BARRIER() __builtin_amdgcn_s_barrier()
-#define KQ_READ(F, r, slice, s) KQ_READC(F, r, 0, slice, s)
-#define KQ_MMA(F, m) Unit::step(acc[(m) >> 2][(m) & 3], &F[((m) >> 2) * CH], &F[(4 + ((m) & 3)) * CH])
-  // fragments in the order the next step's MFMAs use them: A0 B0 B1 B2 B3 A1 A2 A3
-#define KQ_ORDER(x) ((x) == 0 ? 0 : (x) <= 4 ? 4 + (x) - 1 : (x) - 4)
-  // steps 0-2: after MFMA m, the next step's fragment m / 2 (m even); item 4 s + m / 4 of this wave's share of
-  // slice kt + 1 written (m % 4 == 1) and then reloaded with slice `ls` (m % 4 == 3)
-#define KQ_STEP(CUR, NXT, s, kt, ls)                                                                           \
-  do {                                                                                                         \
-    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
-      KQ_MMA(CUR, m);                                                                                          \
-      KQ_FENCE();                                                                                              \
-      if (m % 2 == 0) { KQ_READ(NXT, KQ_ORDER(m / 2), kt, (s) + 1); KQ_FENCE(); }                             \
-      if (m % 4 == 1) { KQ_WRITE((s) * 4 + m / 4, (kt) + 1); KQ_FENCE(); }                                    \
-      if (m % 4 == 3) { KQ_LOAD((s) * 4 + m / 4, ls); KQ_FENCE(); }                                           \
-    }                                                                                                          \
-  } while (0)
-  // step 3: items 12-15 written under the first four MFMAs and reloaded under the next four, then the barrier
-  // (this wave's LDS traffic done, its last write four MFMAs old), then the first fragments of slice kt + 1 under
-  // the last eight
-#define KQ_STEP3(CUR, NXT, kt, ls)                                                                             \
-  do {                                                                                                         \
-    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
-      KQ_MMA(CUR, m);                                                                                          \
-      KQ_FENCE();                                                                                              \
-      if (m < 4) { KQ_WRITE(12 + m, (kt) + 1); KQ_FENCE(); }                                                   \
-      if (m >= 4 && m < 8) { KQ_LOAD(8 + m, ls); KQ_FENCE(); }                                                 \
-      if (m == 7) {                                                                                            \
-        __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0), vmcnt and expcnt left alone */                     \
-        KQ_BARRIER();                                                                                          \
-        KQ_FENCE();                                                                                            \
-      }                                                                                                        \
-      if (m >= 7 && m < 15) { KQ_READ(NXT, KQ_ORDER(m - 7), (kt) + 1, 0); KQ_FENCE(); }                       \
-    }                                                                                                          \
-  } while (0)
-  // fp8 (two steps of 64-cycle MFMAs per slice). Step 0: after MFMA m the next step's fragment chunk m (of
-  // KQ_ORDER(m / 2)), item m of slice kt + 1 written (m < 12) and item m - 2 reloaded with slice `ls`.
-#define KQ8_STEP0(CUR, NXT, kt, ls)                                                                            \
-  do {                                                                                                         \
-    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
-      KQ_MMA(CUR, m);                                                                                          \
-      KQ_FENCE();                                                                                              \
-      KQ_READC(NXT, KQ_ORDER(m / 2), m % 2, kt, 1);                                                            \
-      KQ_FENCE();                                                                                              \
-      if (m < 12) { KQ_WRITE(m, (kt) + 1); KQ_FENCE(); }                                                       \
-      if (m >= 2 && m < 14) { KQ_LOAD(m - 2, ls); KQ_FENCE(); }                                                \
-    }                                                                                                          \
-  } while (0)
-  // step 1: items 12-15 written under the first four MFMAs, the barrier after the eighth, then the first step's
-  // fragments of slice kt + 1 (two chunks per MFMA) and the reloads of items 12-15
-#define KQ8_STEP1(CUR, NXT, kt, ls)                                                                            \
-  do {                                                                                                         \
-    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                                           \
-      KQ_MMA(CUR, m);                                                                                          \
-      KQ_FENCE();                                                                                              \
-      if (m < 4) { KQ_WRITE(12 + m, (kt) + 1); KQ_FENCE(); }                                                   \
-      if (m == 7) {                                                                                            \
-        __builtin_amdgcn_s_waitcnt(0xc07f);                                                                    \
-        __builtin_amdgcn_s_barrier();                                                                          \
-        KQ_FENCE();                                                                                            \
-      }                                                                                                        \
-      if (m >= 7 && m < 15) {                                                                                  \
-        KQ_READC(NXT, KQ_ORDER(m - 7), 0, (kt) + 1, 0);                                                        \
-        KQ_READC(NXT, KQ_ORDER(m - 7), 1, (kt) + 1, 0);                                                        \
-        KQ_FENCE();                                                                                            \
-        if (m < 11) { KQ_LOAD(12 + m - 7, ls); KQ_FENCE(); }                                                   \
-      }                                                                                                        \
-    }                                                                                                          \
-  } while (0)
-  // slice 0 through set 0 into stage 0; slices 1 .. NSET into the sets (set of slice j: j % NSET). With two sets,
-  // slice 1 is in flight while slice 0 lands.
-  {
-    constexpr int SET_ = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) KQ_LOAD(q, 0);
-  }
-  if constexpr (NSET == 2) {
-    constexpr int SET_ = 1;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) KQ_LOAD(q, min(1, nk - 1));
-  }
-  {
-    constexpr int SET_ = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) KQ_WRITE(q, 0);
-  }
-  {
-    constexpr int SET_ = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) KQ_LOAD(q, min(NSET, nk - 1));
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_s_barrier();
-  // in the order the loop's last step reads them, so that the first MFMAs wait on a partial LDS count in every
-  // iteration (a reordered prologue forces a full wait at the top of the loop)
-  KQ_FENCE();
-#pragma unroll
-  for (int x = 0; x < 8; ++x)
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      KQ_READC(F0, KQ_ORDER(x), c, 0, 0);
-      KQ_FENCE();
-    }
-  // slice kt writes slice kt + 1 from set (kt + 1) % NSET and reloads that set with slice kt + 1 + NSET
-  if constexpr (NS == 4) {
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-      {
-        constexpr int SET_ = 1;
-        const int ls = min(kt + 3, nk - 1);
-        KQ_STEP(F0, F1, 0, kt, ls);
-        KQ_STEP(F1, F0, 1, kt, ls);
-        KQ_STEP(F0, F1, 2, kt, ls);
-        KQ_STEP3(F1, F0, kt, ls);
-      }
-      {
-        constexpr int SET_ = 0;
-        const int ls = min(kt + 4, nk - 1);
-        KQ_STEP(F0, F1, 0, kt + 1, ls);
-        KQ_STEP(F1, F0, 1, kt + 1, ls);
-        KQ_STEP(F0, F1, 2, kt + 1, ls);
-        KQ_STEP3(F1, F0, kt + 1, ls);
-      }
-    }
-    if (kt < nk) {
-      constexpr int SET_ = 1;
-      const int ls = nk - 1;
-      KQ_STEP(F0, F1, 0, kt, ls);
-      KQ_STEP(F1, F0, 1, kt, ls);
-      KQ_STEP(F0, F1, 2, kt, ls);
-      KQ_STEP3(F1, F0, kt, ls);
-    }
-  } else {
-    constexpr int SET_ = 0;
-    for (int kt = 0; kt < nk; ++kt) {
-      const int ls = min(kt + 2, nk - 1);
-      KQ8_STEP0(F0, F1, kt, ls);
-      KQ8_STEP1(F1, F0, kt, ls);
-    }
-  }
-#undef KQ_LOAD
-#undef KQ_WRITE
-#undef KQ_READ
-#undef KQ_READC
-#undef KQ8_STEP0
-#undef KQ8_STEP1
-#undef KQ_FENCE
-#undef KQ_BARRIER
-#undef KQ_MMA
-#undef KQ_ORDER
-#undef KQ_STEP
-#undef KQ_STEP3
-  __syncthreads();  // every wave is done with the stages before its LDS becomes the store patches
-  uint32_t* patch = reinterpret_cast<uint32_t*>(lds) + wave * PATCH_WORDS;
-  store_tile<FMT == FMT_I8, 4, 4, Acc, true>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
-}
-
-#ifndef KRN_D16_NOLOAD
-#define KRN_D16_NOLOAD 0
-#endif
-// Four-wave main loop for whole 256 x 256 tiles of 16-bit operands (NT) with the 16x16x32 MFMA form and
-// direct-to-LDS slices. Each wave owns a 128 x 128 quarter (wave w: rows 128 (w >> 1), columns 128 (w & 1)) as
-// 8 x 8 accumulator blocks of 16 x 16 in AGPRs. 128-byte K slices go straight from global memory into LDS stages, NA
-// for A and NB for B (2 or 3; 3 + 2 stages of 32 KiB fill the 160 KiB), each stage a separate array so that the
-// compiler can tell every fragment read from the loads in flight into the other stages; wave w loads rows
-// 64 w .. 64 w + 63 of A and of B, 8 rows (1 KiB) per load, chunk c of row r at slot c ^ ((r >> 1) & 7).
-//
-// A slice is two steps of 32 K. One set of fragments (A blocks 0-3 and B blocks 0-3, each two 16-row halves) is
-// refilled in place: step 0 runs its 16 blocks of 32 x 32 row by row (block (I, J) is group 4 I + J of four
-// MFMAs), step 1 column by column, so a block's fragments are dead after its last group of the step and take the
-// next step's at once (step 0 frees A block I after group 4 I + 3 and B block J after 12 + J; step 1 frees B block
-// J after 4 J + 3 and A block I after 12 + I). The one barrier per slice sits after group 3 of step 1: by then
-// this wave has read all of slice kt (its step-1 fragments were read during step 0) and its loads of slice kt + 1
-// have landed; after it the loads of slice kt + N of an operand with N stages go into the stage slice kt leaves,
-// and the fragments of slice kt + 1 are read as step 1 frees their registers. An operand's slice thus has N - 1
-// slices of MFMA time to arrive.
-template <int FMT, int NA = 2, int NB = 2, bool NN = false>
-__global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
+__global__ __launch_bounds__(256, 1) void gemm_quad16(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B,
                                                      void* __restrict__ C, int64_t M, int64_t N, int64_t kbytes,
                                                      int64_t lda, int64_t ldb, int64_t ldc, Epilogue e) {
-  static_assert((NA == 2 || NA == 3) && (NB == 2 || NB == 3) && NA + NB <= 5, "stages: 160 KiB of LDS");
+  constexpr int NA = 2, NB = 3;  // LDS stages of A and B
   typedef Mfma16<FMT> Unit;
   typedef typename Unit::Acc Acc;
   typedef typename Mfma<FMT>::Acc Acc32;
-  static_assert(FMT == FMT_BF16 || FMT == FMT_F16, "16-bit operands");
+  // fp8: one 16x16x128 step per slice, 32 bytes of K per lane and operand; otherwise two steps of 16 bytes
+  constexpr bool F8 = FMT == FMT_FP8;
+  constexpr int NSTEP = F8 ? 1 : 2;
+  typedef typename std::conditional<F8, i32x8, u32x4>::type Frag;
+  static_assert(!NN || FMT == FMT_BF16 || FMT == FMT_F16, "NN: 16-bit operands");
   constexpr int BM = 256, BN = 256, BKB = 128;
   constexpr int HALF = BM * BKB;  // 32 KiB: one operand's rows of one slice
-  constexpr int UNROLL = NA == NB ? 2 : 6;  // slices per loop iteration: every stage index a constant
+  constexpr int UNROLL = 6;  // slices per loop iteration: every stage index a constant
   __shared__ __attribute__((aligned(1024))) uint8_t la0[HALF];
   __shared__ __attribute__((aligned(1024))) uint8_t la1[HALF];
-  __shared__ __attribute__((aligned(1024))) uint8_t la2[NA == 3 ? HALF : 16];
   __shared__ __attribute__((aligned(1024))) uint8_t lb0[HALF];
   __shared__ __attribute__((aligned(1024))) uint8_t lb1[HALF];
-  __shared__ __attribute__((aligned(1024))) uint8_t lb2[NB == 3 ? HALF : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t lb2[HALF];
   int tm, tn;
   tile_of((int)((M + BM - 1) / BM), (int)((N + BN - 1) / BN), tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -1358,24 +1102,27 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
   const int tr_row = (8 * tg + (ta >> 2)) * 512, tr_swz = nn_swz(8 * tg + (ta >> 2));
   const int tr_col = wn * 128 + 4 * (ta & 3);
   const int wbase = wave * 8192;
-  // fragment bases: lane L reads row L & 15 of a 16-row half, 16-byte chunk 4 s + (L >> 4) (step s)
+  // fragment bases: lane L reads row L & 15 of a 16-row half, 16-byte chunk 4 x + (L >> 4) (step x), or for fp8
+  // chunks 2 (L >> 4) + x (x = 0, 1: the lane's 32 bytes)
   int ra[2], rb[2];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int part = (lane & 15) * 128 + (((4 * s + (lane >> 4)) ^ (((lane & 15) >> 1) & 7)) * 16);
-    ra[s] = part + wm * 128 * 128;
-    rb[s] = part + wn * 128 * 128;
+  for (int x = 0; x < 2; ++x) {
+    const int chunk = F8 ? 2 * (lane >> 4) + x : 4 * x + (lane >> 4);
+    const int part = (lane & 15) * 128 + ((chunk ^ (((lane & 15) >> 1) & 7)) * 16);
+    ra[x] = part + wm * 128 * 128;
+    rb[x] = part + wn * 128 * 128;
   }
+  const int one = 127;  // fp8: the unit E8M0 scale
   const int nk = (int)(kbytes / BKB);  // >= 2 (host)
 
-  u32x4 F[16];  // A block I half R at 2 I + R, B block J half Q at 8 + 2 J + Q
+  Frag F[16];  // A block I half R at 2 I + R, B block J half Q at 8 + 2 J + Q
   Acc acc[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = Acc{};
 
-#define KD_A(p) ((p) == 0 ? la0 : (p) == 1 ? la1 : la2)
+#define KD_A(p) ((p) == 0 ? la0 : la1)
 #define KD_B(p) ((p) == 0 ? lb0 : (p) == 1 ? lb1 : lb2)
 #define KD_LOADA(j, sl, pa)                                                                                    \
   buffer_to_lds16(a_rsrc, KD_A(pa) + wbase + (j) * 1024, ga[(j) & 1], (int)((sl) * BKB + ((j) & 6) * 8 * lda))
@@ -1394,19 +1141,31 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
                                 ((((col) >> 3) ^ tr_swz) * 16) + ((col) & 7) * 2)))
 #define KD_READ(r, c, pa, pb, s)                                                                               \
   do {                                                                                                         \
-    if (NN && (r) >= 4) {                                                                                      \
-      const int col = tr_col + ((r) - 4) * 32 + (c) * 16;                                                      \
-      const u32x2 lo = KD_TR(pb, s, 0, col), hi = KD_TR(pb, s, 1, col);                                        \
-      F[(r) * 2 + (c)] = u32x4{lo[0], lo[1], hi[0], hi[1]};                                                    \
+    if constexpr (F8) {                                                                                        \
+      const uint8_t* p8 = ((r) < 4 ? KD_A(pa) : KD_B(pb)) + (((r) & 3) * 32 + (c) * 16) * 128;                 \
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(p8 + ((r) < 4 ? ra[0] : rb[0]));                        \
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(p8 + ((r) < 4 ? ra[1] : rb[1]));                        \
+      F[(r) * 2 + (c)] = Frag{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],                                   \
+                              (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};                                 \
     } else {                                                                                                   \
-      F[(r) * 2 + (c)] = *reinterpret_cast<const u32x4*>(                                                      \
-          ((r) < 4 ? KD_A(pa) + ra[s] : KD_B(pb) + rb[s]) + (((r) & 3) * 32 + (c) * 16) * 128);                \
+      if (NN && (r) >= 4) {                                                                                    \
+        const int col = tr_col + ((r) - 4) * 32 + (c) * 16;                                                    \
+        const u32x2 lo = KD_TR(pb, s, 0, col), hi = KD_TR(pb, s, 1, col);                                      \
+        F[(r) * 2 + (c)] = u32x4{lo[0], lo[1], hi[0], hi[1]};                                                  \
+      } else {                                                                                                 \
+        F[(r) * 2 + (c)] = *reinterpret_cast<const u32x4*>(                                                    \
+            ((r) < 4 ? KD_A(pa) + ra[s] : KD_B(pb) + rb[s]) + (((r) & 3) * 32 + (c) * 16) * 128);              \
+      }                                                                                                        \
     }                                                                                                          \
   } while (0)
 #define KD_FENCE() __builtin_amdgcn_sched_barrier(0)
 #define KD_MMA(I, J)                                                                                           \
-  _Pragma("unroll") for (int R = 0; R < 2; ++R) _Pragma("unroll") for (int Q = 0; Q < 2; ++Q)                 \
-      Unit::step_agpr(acc[(I) * 2 + R][(J) * 2 + Q], F[(I) * 2 + R], F[8 + (J) * 2 + Q])
+  _Pragma("unroll") for (int R = 0; R < 2; ++R) _Pragma("unroll") for (int Q = 0; Q < 2; ++Q) {               \
+    if constexpr (F8)                                                                                          \
+      Unit::step_agpr(acc[(I) * 2 + R][(J) * 2 + Q], F[(I) * 2 + R], F[8 + (J) * 2 + Q], one);                \
+    else                                                                                                       \
+      Unit::step_agpr(acc[(I) * 2 + R][(J) * 2 + Q], F[(I) * 2 + R], F[8 + (J) * 2 + Q]);                     \
+  }
   // One step of slice kt (A stage PA, B stage PB). ORD 0: its 16 blocks row by row (group g = 4 I + J), 1: column
   // by column (g = 4 J + I); either way A block I is dead after its group with J = 3 and B block J after its group
   // with I = 3, and the next step's fragments of that block are read at once (ORD 0 reads A first, 1 reads B first).
@@ -1423,22 +1182,21 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
       KD_MMA(I, J);                                                                                            \
       KD_FENCE();                                                                                              \
       if ((LAST) && g == 3) {                                                                                  \
-        if constexpr (NA == 3 || NB == 3)                                                                      \
-          __builtin_amdgcn_s_waitcnt(0x0070 | 8); /* vmcnt(8) lgkmcnt(0) */                                     \
+        /* still in flight may be only B's slice kt + 2: its loads of step 0 (eight), or of this step's groups 0  \
+           and 2 (fp8) */                                                                                      \
+        if constexpr (NSTEP == 1)                                                                              \
+          __builtin_amdgcn_s_waitcnt(0x0070 | 2); /* vmcnt(2) lgkmcnt(0) */                                     \
         else                                                                                                   \
-          __builtin_amdgcn_s_waitcnt(0x0070); /* vmcnt(0) lgkmcnt(0) */                                         \
+          __builtin_amdgcn_s_waitcnt(0x0070 | 8); /* vmcnt(8) lgkmcnt(0) */                                     \
         __builtin_amdgcn_s_barrier();                                                                          \
         KD_FENCE();                                                                                            \
       }                                                                                                        \
-      if ((LAST) && !KRN_D16_NOLOAD && g >= 3 && g < 11) {                                                     \
-        const int j = 2 * (g - 3);                                                                             \
-        if ((j < 8) == (NB <= NA)) {                                                                           \
-          KD_LOADB(j & 7, min((kt) + NB, nk - 1), PB);                                                         \
-          KD_LOADB((j & 7) + 1, min((kt) + NB, nk - 1), PB);                                                   \
-        } else {                                                                                               \
-          KD_LOADA(j & 7, min((kt) + NA, nk - 1), PA);                                                         \
-          KD_LOADA((j & 7) + 1, min((kt) + NA, nk - 1), PA);                                                   \
-        }                                                                                                      \
+      if ((NSTEP == 1 || !(LAST)) && (NSTEP == 1 ? (g & 1) == 0 : (g & 1))) {                                  \
+        KD_LOADB(g >> 1, min((kt) + 2, nk - 1), ((PB) + 2) % NB);                                              \
+        KD_FENCE();                                                                                            \
+      }                                                                                                        \
+      if ((LAST) && g >= 3 && g < 11) {                                                                        \
+        KD_LOADA(g - 3, min((kt) + 2, nk - 1), PA);                                                            \
         KD_FENCE();                                                                                            \
       }                                                                                                        \
       _Pragma("unroll") for (int o = 0; o < 2; ++o) {                                                          \
@@ -1455,36 +1213,28 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
       }                                                                                                        \
     }                                                                                                          \
   } while (0)
-  // slice u of an unrolled run: step 0 row by row, step 1 column by column
+  // slice u of an unrolled run (u even at the start of a run, so that the order alternates from step to step):
+  // step 0 row by row, step 1 column by column; fp8's one step per slice alternates from slice to slice
 #define KD_SLICE(u, kt)                                                                                        \
   do {                                                                                                         \
-    KD_STEP((u) % NA, (u) % NB, 0, false, kt, 0);                                                              \
-    KD_STEP((u) % NA, (u) % NB, 1, true, kt, 1);                                                               \
+    if constexpr (NSTEP == 2) {                                                                                \
+      KD_STEP((u) % NA, (u) % NB, 0, false, kt, 0);                                                            \
+      KD_STEP((u) % NA, (u) % NB, 1, true, kt, 1);                                                             \
+    } else {                                                                                                   \
+      KD_STEP((u) % NA, (u) % NB, (u) & 1, true, kt, 0);                                                       \
+    }                                                                                                          \
   } while (0)
 
-  // the prologue: the first NA slices of A and NB of B, slice by slice (a three-stage operand's third slice last,
-  // as in the loop); once slice 0 has landed everywhere, its step-0 fragments
+  // the prologue: slices 0 and 1 of A and B (B's slice 2 loads during slice 0, as in the loop); once slice 0 has
+  // landed everywhere, its step-0 fragments
 #pragma unroll
-  for (int sl = 0; sl < 3; ++sl) {
-    if (sl < NA - (NA == 3)) {
+  for (int sl = 0; sl < 2; ++sl) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) KD_LOADA(j, min(sl, nk - 1), sl);
-    }
-    if (sl < NB - (NB == 3)) {
+    for (int j = 0; j < 8; ++j) KD_LOADA(j, min(sl, nk - 1), sl);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) KD_LOADB(j, min(sl, nk - 1), sl);
-    }
+    for (int j = 0; j < 8; ++j) KD_LOADB(j, min(sl, nk - 1), sl);
   }
-  if constexpr (NA == 3) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) KD_LOADA(j, min(2, nk - 1), 2);
-  }
-  if constexpr (NB == 3) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) KD_LOADB(j, min(2, nk - 1), 2);
-  }
-  // slice 0's 16 loads came first
-  __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | (NA + NB == 5 ? 24 : 16));
+  __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | 16);  // vmcnt(16): slice 0's loads came first
   __builtin_amdgcn_s_barrier();
   KD_FENCE();
   // in the order step 1 reads them (B0 B1 B2 A0 A1 A2 B3 A3), so that the loop's first MFMAs wait on the same
@@ -1520,7 +1270,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dtl16(const uint8_t* __restrict__
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   __syncthreads();  // every wave is done with the stages before their LDS becomes the store patches
   uint32_t* patch = reinterpret_cast<uint32_t*>(la0) + wave * PATCH_WORDS;
-  store_tile16<false, 4, 4, Acc32>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
+  store_tile16<FMT == FMT_I8, 4, 4, Acc32>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
 }
 
 // Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
@@ -1857,39 +1607,15 @@ static int launch_pipe(const void* a, const void* b, void* c, int64_t m, int64_t
 }
 
 template <int FMT>
-static int launch_quad(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
-                       int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
+static int launch_quad16(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
+                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
   const int64_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
   if (tiles > 0x7fffffff) {
     krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
     return -1;
   }
-  hipLaunchKernelGGL((gemm_quad<FMT>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
+  hipLaunchKernelGGL((gemm_quad16<FMT>), dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)a,
                      (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) {
-    krn_set_error("gemm launch: %s", hipGetErrorString(err));
-    return (int)err;
-  }
-  return 0;
-}
-
-#ifndef KRN_D16_NA
-#define KRN_D16_NA 2
-#endif
-#ifndef KRN_D16_NB
-#define KRN_D16_NB 3
-#endif
-template <int FMT>
-static int launch_dtl16(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
-                        int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  const int64_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
-  if (tiles > 0x7fffffff) {
-    krn_set_error("gemm: %lld tiles exceed the grid limit", (long long)tiles);
-    return -1;
-  }
-  hipLaunchKernelGGL((gemm_dtl16<FMT, KRN_D16_NA, KRN_D16_NB>), dim3((unsigned)tiles), dim3(256), 0, stream,
-                     (const uint8_t*)a, (const uint8_t*)b, c, m, n, kbytes, lda, ldb, ldc, e);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     krn_set_error("gemm launch: %s", hipGetErrorString(err));
@@ -1972,29 +1698,19 @@ static int launch_skinny(const void* a, const void* b, void* c, int64_t m, int64
   return -1;
 }
 
-// 256 x 256 tiles (ragged at the edges): for bf16/f16 the four-wave loop over register-staged 128-byte slices (K of
-// at least two slices; otherwise a ring of four 64-byte slices); for fp8 the ping-pong ring of four 64-byte slices
-// (one MFMA step each); for int8 two 128-byte slices of the eight-wave ring (the four-wave loop is 19 % slower on
-// W8A8 4096 x 14336 x 4096).
+// 256 x 256 tiles (ragged at the edges).
 template <int FMT>
 static int launch_whole(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                         int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
-  // bf16/f16: four waves of 128 x 128 on 16x16x32 MFMAs with direct-to-LDS slices (8192^3 1424 TFLOP/s against
-  // 1335 for the register-staged 32x32 loop). fp8: the register-staged four-wave loop on 32x32x64 MFMAs (7 % faster
-  // than the eight-wave ping-pong, which keeps the one-slice K = 128 case); the direct-to-LDS loop on 16x16x128 ran
-  // at a higher clock with proportionally less MFMA time, equal overall. int8: eight waves (4 x 2, each 64 x 128 of
-  // the tile) that interleave their own LDS reads with their MFMAs (the four-wave register-staged loop 7-10 % and
-  // the direct-to-LDS 16x16x64 loop 2 % slower on W8A8 M = 4096, whose K of 32 slices leaves more of the time to
-  // the prologue and epilogue).
-  if constexpr (FMT == FMT_FP8) {
-    if (kbytes >= 256) return launch_quad<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  // Two slices or more: the four-wave loop on 16x16 MFMAs (gemm_quad16). One slice (K = 128 bytes): fp8 the
+  // eight-wave ping-pong, int8 and bf16/f16 the eight-wave direct-to-LDS ring.
+  if (kbytes >= 256) return launch_quad16<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  if constexpr (FMT == FMT_FP8)
     return launch_pp<FMT, 4>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
-  } else if constexpr (FMT == FMT_I8) {
+  else if constexpr (FMT == FMT_I8)
     return launch_pipe<FMT, 256, 256, 4, 2, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
-  } else {
-    if (kbytes % 128 == 0 && kbytes >= 256) return launch_dtl16<FMT>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+  else
     return launch_pipe<FMT, 256, 256, 4, 2, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
-  }
 }
 
 // Up to one wave of 128 x 128 tiles (at most 256 tiles): the pipelined loop on 128 x 128 tiles with four waves, a
@@ -2164,7 +1880,7 @@ __global__ __launch_bounds__(256) void transpose16(const uint16_t* __restrict__ 
 
 // The NN product `a[rows, ks] @ b[ks, cols]` with B stored K x N: B is transposed into `bt` (N x K, n * k 16-bit
 // elements) and the NT kernels run on it. Both launches go on `stream`, in that order.
-// The NN products the four-wave loop takes with B read K-major from LDS (no transposed copy): at least 128 tiles
+// The NN products gemm_quad16 takes with B read K-major from LDS (no transposed copy): at least 128 tiles
 // of 256 x 256, N a multiple of 256, K of 64 (whole 128-byte slices, at least two), 16-byte aligned operands, and
 // panels addressable by 31-bit buffer offsets.
 static bool nn_direct(const void* a, const void* b, int64_t m, int64_t n, int64_t k) {
@@ -2193,22 +1909,11 @@ static int gemm_nn_through(int in_kind, const void* a, const void* b, void* c, i
       return -1;
     }
     const int64_t tiles = ((m + 255) / 256) * (n / 256);
-#ifndef KRN_NN_DTL
-#define KRN_NN_DTL 1
-#endif
-    if (KRN_NN_DTL && in_kind == BF16)
-      hipLaunchKernelGGL((gemm_dtl16<FMT_BF16, KRN_D16_NA, KRN_D16_NB, true>), dim3((unsigned)tiles), dim3(256), 0,
-                         (hipStream_t)stream, (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n,
-                         e);
-    else if (KRN_NN_DTL)
-      hipLaunchKernelGGL((gemm_dtl16<FMT_F16, KRN_D16_NA, KRN_D16_NB, true>), dim3((unsigned)tiles), dim3(256), 0,
-                         (hipStream_t)stream, (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n,
-                         e);
-    else if (in_kind == BF16)
-      hipLaunchKernelGGL((gemm_quad<FMT_BF16, true>), dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
+    if (in_kind == BF16)
+      hipLaunchKernelGGL((gemm_quad16<FMT_BF16, true>), dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
                          (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n, e);
     else
-      hipLaunchKernelGGL((gemm_quad<FMT_F16, true>), dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
+      hipLaunchKernelGGL((gemm_quad16<FMT_F16, true>), dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
                          (const uint8_t*)a, (const uint8_t*)b, c, m, n, k * 2, k * 2, n * 2, n, e);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) {
