@@ -3,12 +3,12 @@
 // This is the lowering of krn's tile contraction `acc += a[rows, ks] @ b[cols, ks].transpose()` followed by
 // `c[rows, cols] = f(acc).to(dtype)` (reference compiler/ir.py:309-315 Accumulate, compiler/emit.py:788-821). One
 // workgroup owns a BM x BN output tile split among its waves, and every wave keeps its accumulators in registers as
-// 32x32 MFMA blocks (or four 16x16 blocks joined into that layout when stored). Main loops: `gemm_quad16` (every
+// 32x32 MFMA blocks (`gemm_quad16`: 16x16 blocks of the transposed product). Main loops: `gemm_quad16` (every
 // format, also the bf16/f16 NN form, 16x16 MFMAs) for whole 256 x 256 tiles of two K slices or more, `gemm_pipe`
 // and `gemm_pp` (fp8) for one slice and, `gemm_pipe`, on 128 x 128 and 128 x 256 tiles for mid-size products,
 // `gemm_skinny` for M <= 128 (rings of direct-to-LDS slices per wave), and `gemm_tile` for the rest (128-byte
-// slices staged through registers, bounds-checked, double buffered). All end in `store_tile`: whole blocks straight
-// from the accumulators (the direct epilogue), the rest through an LDS patch.
+// slices staged through registers, bounds-checked, double buffered). All end in `store_tile` (`gemm_quad16`:
+// `store_tile16t`): whole blocks straight from the accumulators (the direct epilogue), the rest through an LDS patch.
 //
 // One byte-oriented main loop serves three operand formats, because each MFMA consumes the same 16 bytes per lane
 // per half-wave:
@@ -386,9 +386,8 @@ __device__ __forceinline__ void store_block(const V& block, uint32_t* patch, voi
 // patch, for epilogues of at most two operations that are float32 scalars or row/column vectors (no activation):
 // the headline bf16 product, the fp8 product's `acc * (scale_a * scale_b)`, the W8A8 dequantisation
 // `acc * scale_a[m] * scale_w[n]`. Lane L holds column c = L & 31 at rows R(r) = (r / 4) * 8 + (L / 32) * 4 + r % 4;
-// neighbouring lanes hold columns c and c ^ 1 of the same rows. Blocks go out in pairs (store_pair_direct), so that
-// each store instruction writes whole 128-byte lines: non-temporal half lines cost a third more HBM writes. The
-// operations and their rounding are the patch path's, so the result is the same bit for bit.
+// neighbouring lanes hold columns c and c ^ 1 of the same rows. The operations and their rounding are the patch
+// path's, so the result is the same bit for bit.
 constexpr int DIRECT_OPS = 2;
 
 __device__ __forceinline__ bool direct_epilogue(const Epilogue& e) {
@@ -480,41 +479,13 @@ __device__ __forceinline__ void store_block_direct(const V& block, const DirectV
   }
 }
 
-// Blocks (i, j) and (i, j + 1), j even: 64 columns, one 128-byte line of 16-bit C per row. For every accumulator
-// register r (row R(r)) the even lane keeps its block-j value of column c and takes column c + 1 of block j from
-// lane c + 1, the odd lane keeps its block-(j + 1) value and takes column c - 1 of block j + 1 from lane c - 1 (one
-// DPP swap): the even lanes of a half-wave then hold block j of row R(r) and the odd lanes block j + 1, so each
-// 4-byte store instruction writes whole 128-byte lines (two rows), never a half line.
-template <bool INT, bool BF, int TM, int TN, typename V>
-__device__ __forceinline__ void store_pair_direct(const V& b0, const V& b1, const DirectVectors<TM, TN>& dv, int i,
-                                                  int j, __amdgpu_buffer_rsrc_t out, uint32_t lane_off, int64_t ldc,
-                                                  const Epilogue& e, int lane) {
-  float v0[16], v1[16];
-  direct_ops<INT>(v0, b0, dv, i, j, e);
-  direct_ops<INT>(v1, b1, dv, i, j + 1, e);
-  const int odd = lane & 1;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const float send = odd ? v0[r] : v1[r];
-    // quad_perm [1, 0, 3, 2]: exchange with lane ^ 1
-    const float recv = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, true));
-    const float lo = odd ? recv : v0[r], hi = odd ? v1[r] : recv;
-    const uint32_t pair = BF ? f2bf2(lo, hi) : ((uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16));
-    // register r holds row (r >> 2) * 8 + half * 4 + (r & 3): the lane's part (half * 4, its column pair and
-    // block) is in lane_off, the rest is the same for the whole wave, a scalar offset
-    const int step = (r >> 2) * 8 + (r & 3) + i * 32;
-    const int soff = __builtin_amdgcn_readfirstlane((int)(((int64_t)step * ldc + j * 32) * 2));
-    __builtin_amdgcn_raw_buffer_store_b32(pair, out, (int)lane_off, soff, 2 /* nt */);
-  }
-}
-
 // A wave's TM x TN accumulator blocks to C. When the wave's whole region lies inside C and the epilogue is one the
 // direct path takes, every block goes straight from registers; otherwise each block goes through the LDS patch (all
 // operations, ragged edges, int32 and float32 outputs).
-//
-// AGPR: the accumulators live in AGPRs (the four-wave loop's 256 of them). Each block is then copied to VGPRs right
-// before it is stored, by ordered reads; left to itself the compiler copies all of them at the end of the loop and
-// spills most of them to private memory.
+
+// A block of accumulators held in AGPRs (the four-wave loop's 256 of them), copied to VGPRs right before it is
+// stored, by ordered reads; left to itself the compiler copies all of them at the end of the loop and spills most of
+// them to private memory.
 template <typename V>
 __device__ __forceinline__ V agpr_block(const V& x) {
   V y;
@@ -524,8 +495,8 @@ __device__ __forceinline__ V agpr_block(const V& x) {
   return y;
 }
 
-// `fetch(i, j)` hands over block (i, j) in the 32x32 accumulator layout; AGPR: blocks are stored in pairs.
-template <bool INT, int TM, int TN, bool AGPR, typename Fetch>
+// `fetch(i, j)` hands over block (i, j) in the 32x32 accumulator layout.
+template <bool INT, int TM, int TN, typename Fetch>
 __device__ __forceinline__ void store_tile_by(Fetch fetch, uint32_t* patch, void* C, int64_t ldc, int64_t row0,
                                               int64_t col0, int64_t M, int64_t N, const Epilogue& e, int lane) {
   const bool direct = direct_epilogue(e) && (ldc % 2) == 0 && (uintptr_t)C % 4 == 0 && row0 + 32 * TM <= M &&
@@ -543,22 +514,12 @@ __device__ __forceinline__ void store_tile_by(Fetch fetch, uint32_t* patch, void
     const uint32_t base_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
     const void* region = (const void*)(((uint64_t)base_hi << 32) | (uint64_t)base_lo);
     const __amdgpu_buffer_rsrc_t out = panel_rsrc(region, (int64_t)32 * TM * ldc * 2);
-    // AGPR (the four-wave loop): blocks in pairs, whole lines; the lane's row (half * 4) and its column pair
-    // (c & ~1) in block j (even lanes) or j + 1 (odd lanes). Otherwise block by block (measured 3 % faster for
-    // W8A8 on the eight-wave int8 loop, whose registers are tighter): row half * 4 + (c & 1), pair c & ~1.
-    const uint32_t lane_off = AGPR ? (uint32_t)((((lane >> 5) * 4) * ldc + (c & ~1) + (c & 1) * 32) * 2)
-                                   : (uint32_t)((((lane >> 5) * 4 + (c & 1)) * ldc + (c & ~1)) * 2);
-    static_assert(!AGPR || TN % 2 == 0, "blocks stored in pairs");
+    // block by block: row half * 4 + (c & 1), column pair c & ~1 (measured 3 % faster for W8A8 on the eight-wave
+    // int8 loop, whose registers are tighter, than pairs of blocks stored as whole lines)
+    const uint32_t lane_off = (uint32_t)((((lane >> 5) * 4 + (c & 1)) * ldc + (c & ~1)) * 2);
 #define KRN_DIRECT(BF)                                                                                       \
-  _Pragma("unroll") for (int i = 0; i < TM; ++i) {                                                           \
-    if constexpr (AGPR) {                                                                                    \
-      _Pragma("unroll") for (int j = 0; j < TN; j += 2)                                                      \
-        store_pair_direct<INT, BF>(fetch(i, j), fetch(i, j + 1), dv, i, j, out, lane_off, ldc, e, lane);     \
-    } else {                                                                                                 \
-      _Pragma("unroll") for (int j = 0; j < TN; ++j)                                                         \
-        store_block_direct<INT, BF>(fetch(i, j), dv, i, j, out, lane_off, ldc, e, lane);                     \
-    }                                                                                                        \
-  }
+  _Pragma("unroll") for (int i = 0; i < TM; ++i) _Pragma("unroll") for (int j = 0; j < TN; ++j)              \
+      store_block_direct<INT, BF>(fetch(i, j), dv, i, j, out, lane_off, ldc, e, lane);
     if (e.out_kind == BF16) {
       KRN_DIRECT(true)
     } else {
@@ -577,31 +538,143 @@ __device__ __forceinline__ void store_tile_by(Fetch fetch, uint32_t* patch, void
     for (int j = 0; j < TN; ++j) store_block<INT>(fetch(i, j), patch, C, ldc, row0 + i * 32, col0 + j * 32, M, N, local, lane);
 }
 
-template <bool INT, int TM, int TN, typename Acc, bool AGPR = false>
+template <bool INT, int TM, int TN, typename Acc>
 __device__ __forceinline__ void store_tile(const Acc (&acc)[TM][TN], uint32_t* patch, void* C, int64_t ldc,
                                            int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
                                            int lane) {
-  store_tile_by<INT, TM, TN, AGPR>(
-      [&](int i, int j) {
-        if constexpr (AGPR)
-          return agpr_block(acc[i][j]);
-        else
-          return acc[i][j];
-      },
-      patch, C, ldc, row0, col0, M, N, e, lane);
+  store_tile_by<INT, TM, TN>([&](int i, int j) { return acc[i][j]; }, patch, C, ldc, row0, col0, M, N, e, lane);
 }
 
-// The same for 2 TM x 2 TN blocks of 16 x 16 in AGPRs, joined into 32x32 blocks as they are stored.
-template <bool INT, int TM, int TN, typename V16, typename V4>
-__device__ __forceinline__ void store_tile16(const V4 (&acc)[2 * TM][2 * TN], uint32_t* patch, void* C, int64_t ldc,
-                                             int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
-                                             int lane) {
-  store_tile_by<INT, TM, TN, true>(
-      [&](int i, int j) {
-        return join16<V16>(agpr_block(acc[2 * i][2 * j]), agpr_block(acc[2 * i][2 * j + 1]),
-                           agpr_block(acc[2 * i + 1][2 * j]), agpr_block(acc[2 * i + 1][2 * j + 1]));
-      },
-      patch, C, ldc, row0, col0, M, N, e, lane);
+// Register half of the patch path for a block held transposed: `block` is the 32x32 accumulator layout of the
+// transpose of a C block (lane holds C row lane & 31 and C columns (r/4)*8 + (lane/32)*4 + r%4), written into the
+// patch in C's row-major order.
+template <bool INT, typename V>
+__device__ __forceinline__ void patch_put_t(const V& block, uint32_t* patch, int lane) {
+  const int half = lane >> 5, r32 = lane & 31;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const uint32_t bits = INT ? (uint32_t)block[r] : __float_as_uint(block[r]);
+    patch[r32 * PATCH_STRIDE + (r >> 2) * 8 + half * 4 + (r & 3)] = bits;
+  }
+}
+
+// The four-wave loop's 8 x 8 blocks of 16 x 16, computed transposed (B A^T, so that C's rows lie along the lanes):
+// lane L of block (i, j) holds row 16 i + (L & 15) of the wave's 128 x 128 region and its columns
+// 16 j + 4 (L >> 4) .. + 3, one per register. The four lanes L & 15 + 16 s that share a row exchange 8-byte pieces
+// (two permlane swaps per word), so that each holds 16 contiguous columns of one block and writes them as two
+// 16-byte pieces: per store instruction 64 bytes of each of 16 rows. The untransposed 32x32 layout needs a DPP
+// exchange and three selects per register for whole-line pieces; 8-byte pieces without the exchange were slower
+// (quarter lines). Each epilogue operation is two fused multiply-adds, x * s + (-0) = x * s or x * 1 + s = x + s
+// and the identity x * 1 + (-0), each exact or rounded once, signed zeros included, so the result is the patch
+// path's bit for bit. Everything else (ragged edges, int32 and float32 outputs, activations) goes through the patch:
+// four blocks are joined into the 32x32 layout of the transposed block and written into the patch transposed.
+// Against the 32x32 direct store (same box, bench legs): bf16 8192^3 equal, fp8 8192^3 0.440 -> 0.424 ms,
+// W8A8 M = 4096 0.272 -> 0.247 ms; write-back instead of non-temporal stores: bf16 1.5 % slower.
+template <bool INT, bool BF, typename V4>
+__device__ __forceinline__ void store16t_direct(const V4 (&acc)[8][8], void* C, int64_t ldc, int64_t row0,
+                                                int64_t col0, const Epilogue& e, int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  // per operation: the multiplier and addend of a fused multiply-add per row block (row and scalar operations) and
+  // per column of each column block (column operations); the other of the two is the identity x * 1 + (-0), exact
+  // for every x, so each operation is two fused multiply-adds and no selection
+  float rm[DIRECT_OPS][8], ra[DIRECT_OPS][8], cm[DIRECT_OPS][8][4], ca[DIRECT_OPS][8][4];
+#pragma unroll
+  for (int q = 0; q < DIRECT_OPS; ++q) {
+    if (q >= e.nops) break;
+    const int op = e.op[q] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[q] >> VEC_KIND_SHIFT;
+    const bool mul = op < 3, col = op % 3 == 2;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float s = col ? bits_value(kind, vec_bits(e.vec[q], kind, col0 + 16 * j + 4 * g + c)) : 0.0f;
+        cm[q][j][c] = col && mul ? s : 1.0f;
+        ca[q][j][c] = col && !mul ? s : -0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float s = col ? 0.0f
+                          : op % 3 == 1 ? bits_value(kind, vec_bits(e.vec[q], kind, row0 + 16 * i + r16)) : e.scalar[q];
+      rm[q][i] = !col && mul ? s : 1.0f;
+      ra[q][i] = !col && !mul ? s : -0.0f;
+    }
+  }
+  const uint64_t base = (uint64_t)(static_cast<uint16_t*>(C) + row0 * ldc + col0);
+  const uint32_t base_lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
+  const uint32_t base_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+  const void* region = (const void*)(((uint64_t)base_hi << 32) | (uint64_t)base_lo);
+  const __amdgpu_buffer_rsrc_t out = panel_rsrc(region, (int64_t)128 * ldc * 2);
+  // after the exchange below, lane group g holds the 16 columns of block 4 jj + g of its row: two 16-byte pieces
+  const uint32_t lane_off = (uint32_t)((r16 * ldc + 16 * g) * 2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      uint32_t w[4][2];  // [block jb][word]: columns 16 (4 jj + jb) + 4 g + 2 word .. + 1
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        const int j = 4 * jj + jb;
+        const V4 b = agpr_block(acc[i][j]);
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = INT ? (float)(int32_t)b[c] : (float)b[c];
+#pragma unroll
+        for (int q = 0; q < DIRECT_OPS; ++q) {
+          if (q >= e.nops) break;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            v[c] = __builtin_fmaf(__builtin_fmaf(v[c], rm[q][i], ra[q][i]), cm[q][j][c], ca[q][j][c]);
+        }
+        w[jb][0] = BF ? f2bf2(v[0], v[1]) : ((uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16));
+        w[jb][1] = BF ? f2bf2(v[2], v[3]) : ((uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16));
+      }
+      // a 4 x 4 transpose of 8-byte pieces over the four lane groups (16-lane rows) that share a C row: piece
+      // (group s, block jb) goes to group jb, slot s. permlane16_swap(x, y) leaves [x0 y0 x2 y2] in x and
+      // [x1 y1 x3 y3] in y (16-lane rows), permlane32_swap(x, y) [x0 x1 y0 y1] and [x2 x3 y2 y3].
+      uint32_t t[4][2];  // [slot s][word]: columns 16 (4 jj + g) + 4 s + 2 word .. + 1
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const auto p01 = __builtin_amdgcn_permlane16_swap(w[0][x], w[1][x], false, false);
+        const auto p23 = __builtin_amdgcn_permlane16_swap(w[2][x], w[3][x], false, false);
+        const auto q02 = __builtin_amdgcn_permlane32_swap(p01[0], p23[0], false, false);
+        const auto q13 = __builtin_amdgcn_permlane32_swap(p01[1], p23[1], false, false);
+        t[0][x] = q02[0];
+        t[2][x] = q02[1];
+        t[1][x] = q13[0];
+        t[3][x] = q13[1];
+      }
+      const int soff = __builtin_amdgcn_readfirstlane((int)(((int64_t)16 * i * ldc + 64 * jj) * 2));
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{t[0][0], t[0][1], t[1][0], t[1][1]}, out, (int)lane_off, soff,
+                                             2 /* nt */);
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{t[2][0], t[2][1], t[3][0], t[3][1]}, out, (int)lane_off + 16,
+                                             soff, 2 /* nt */);
+    }
+}
+
+template <bool INT, typename V16, typename V4>
+__device__ __forceinline__ void store_tile16t(const V4 (&acc)[8][8], uint32_t* patch, void* C, int64_t ldc,
+                                              int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
+                                              int lane) {
+  const bool direct = direct_epilogue(e) && (ldc % 4) == 0 && (uintptr_t)C % 8 == 0 && row0 + 128 <= M &&
+                      col0 + 128 <= N && (int64_t)128 * ldc * 2 <= 0x7fffffff;
+  if (direct) {
+    if (e.out_kind == BF16)
+      store16t_direct<INT, true>(acc, C, ldc, row0, col0, e, lane);
+    else
+      store16t_direct<INT, false>(acc, C, ldc, row0, col0, e, lane);
+    return;
+  }
+  const Epilogue local = e;  // taken by address by the out-of-line store
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // the transposed 32x32 block's quarter (h, k) is the transpose of C's quarter (k, h)
+      const V16 blk = join16<V16>(agpr_block(acc[2 * i][2 * j]), agpr_block(acc[2 * i + 1][2 * j]),
+                                  agpr_block(acc[2 * i][2 * j + 1]), agpr_block(acc[2 * i + 1][2 * j + 1]));
+      patch_put_t<INT>(blk, patch, lane);
+      patch_store<INT>(patch, C, ldc, row0 + 32 * i, col0 + 32 * j, M, N, local, lane);
+    }
 }
 
 // 16 bytes of row `base` starting at byte `kb`, zero past the row's end or for a row outside the matrix. VEC: the
@@ -1014,7 +1087,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void gemm_pipe(const uint8_t* __re
 
 // The four-wave main loop for whole 256 x 256 tiles with K a multiple of 128 bytes (bf16/f16 NT and NN, fp8, int8),
 // on the 16x16 MFMA forms. Each wave owns a 128 x 128 quarter (wave w: rows 128 (w >> 1), columns 128 (w & 1)) as
-// 8 x 8 accumulator blocks of 16 x 16 in AGPRs. 128-byte K slices go straight from global memory into LDS stages,
+// 8 x 8 accumulator blocks of 16 x 16 in AGPRs, each computed transposed (B A^T: the B fragment is the MFMA's first
+// operand), so that a lane holds four columns of one row for the store (`store_tile16t`). 128-byte K slices go straight from global memory into LDS stages,
 // two for A and three for B (5 x 32 KiB fill the 160 KiB), each stage a separate array so that the compiler can tell
 // every fragment read from the loads in flight into the other stages; wave w loads rows 64 w .. 64 w + 63 of A and
 // of B, 8 rows (1 KiB) per load, chunk c of row r at slot c ^ ((r >> 1) & 7).
@@ -1162,9 +1236,9 @@ __global__ __launch_bounds__(256, 1) void gemm_quad16(const uint8_t* __restrict_
 #define KD_MMA(I, J)                                                                                           \
   _Pragma("unroll") for (int R = 0; R < 2; ++R) _Pragma("unroll") for (int Q = 0; Q < 2; ++Q) {               \
     if constexpr (F8)                                                                                          \
-      Unit::step_agpr(acc[(I) * 2 + R][(J) * 2 + Q], F[(I) * 2 + R], F[8 + (J) * 2 + Q], one);                \
+      Unit::step_agpr(acc[(I) * 2 + R][(J) * 2 + Q], F[8 + (J) * 2 + Q], F[(I) * 2 + R], one);                \
     else                                                                                                       \
-      Unit::step_agpr(acc[(I) * 2 + R][(J) * 2 + Q], F[(I) * 2 + R], F[8 + (J) * 2 + Q]);                     \
+      Unit::step_agpr(acc[(I) * 2 + R][(J) * 2 + Q], F[8 + (J) * 2 + Q], F[(I) * 2 + R]);                     \
   }
   // One step of slice kt (A stage PA, B stage PB). ORD 0: its 16 blocks row by row (group g = 4 I + J), 1: column
   // by column (g = 4 J + I); either way A block I is dead after its group with J = 3 and B block J after its group
@@ -1272,7 +1346,7 @@ __global__ __launch_bounds__(256, 1) void gemm_quad16(const uint8_t* __restrict_
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   __syncthreads();  // every wave is done with the stages before their LDS becomes the store patches
   uint32_t* patch = reinterpret_cast<uint32_t*>(la0) + wave * PATCH_WORDS;
-  store_tile16<FMT == FMT_I8, 4, 4, Acc32>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
+  store_tile16t<FMT == FMT_I8, Acc32>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
 }
 
 // Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
