@@ -252,7 +252,15 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
       KRN_FA_LOAD(v_rsrc, 0, V_BASE, voff);
       if (ntiles > 1) KRN_FA_LOAD(k_rsrc, 1, TILE_BYTES, koff);
     }
-    KRN_FA_PUBLISH();
+    if (preloaded) {
+      // the last vector memory operations issued are the previous tile's D / 16 output stores (every wave issues
+      // all of them): everything before them, this tile's first K and V tiles included, has landed at vmcnt(D / 16)
+      __builtin_amdgcn_s_waitcnt(0x0070 | 0x0f00 | (D / 16));
+      __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00); /* lgkmcnt(0) */
+      __builtin_amdgcn_s_barrier();
+    } else {
+      KRN_FA_PUBLISH();
+    }
     KRN_FA_SCORES(sa, 0, 0);  // the first half is active for every wave
     KRN_FA_RAWMAX(sa, tmax_next);
   }
@@ -349,6 +357,9 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(total), __float_as_uint(total), false, false);
     total = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
+  // the head's rows of O as a buffer resource: stores of rows past sq fall outside it and are dropped, so every
+  // wave issues the same D / 16 stores whatever its rows (the next tile's first barrier counts on it)
+  const __amdgpu_buffer_rsrc_t o_rsrc = panel_rsrc(o, sq * D * 2);
   const float inv = 1.0f / total;  // one division per row instead of 64 per lane (causal B4 H32 S4096 D128 +2 %)
   // Lane (r32, half) holds columns i * 32 + gq * 8 + half * 4 .. + 3 of its row; its partner lane ^ 32 the other
   // four of each group of eight. One v_permlane32_swap per word pairs them, so that the lower lane owns the eight
@@ -374,7 +385,8 @@ __device__ __forceinline__ void attention_tile(const uint16_t* __restrict__ Q, c
       }
       const int e2 = half;  // the group this lane stores
       const uint4 piece = half ? uint4{got[0], got[1], w[1][0], w[1][1]} : uint4{w[0][0], w[0][1], got[0], got[1]};
-      if (qrow < sq) *reinterpret_cast<uint4*>(o + qrow * D + i * 32 + (2 * gp + e2) * 8) = piece;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, piece), o_rsrc,
+                                             (int)((qrow * D + i * 32 + (2 * gp + e2) * 8) * 2), 0, 0);
     }
 }
 
@@ -452,6 +464,10 @@ extern "C" int krn_attention_fwd(int kind, const void* q, const void* k, const v
   }
   if (sk * d * 2 > 0x7fffffff) {  // K and V tiles are addressed by 31-bit offsets within a head
     krn_set_error("attention: %lld keys of %lld elements exceed 2 GiB per head", (long long)sk, (long long)d);
+    return -1;
+  }
+  if ((sq + BQ) * d * 2 > 0x7fffffff) {  // so are the output rows, those of a last partial query tile included
+    krn_set_error("attention: %lld queries of %lld elements exceed 2 GiB per head", (long long)sq, (long long)d);
     return -1;
   }
   hipStream_t s = (hipStream_t)stream;
