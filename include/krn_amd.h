@@ -96,7 +96,8 @@ int krn_transpose16(const void* in, void* out, int64_t rows, int64_t cols, void*
  * (bh, sq, d) / (bh, sk, d) of kind KRN_BF16 or KRN_F16, d = 64 or 128, 16-byte aligned. `scale` multiplies the
  * scores before exp2 (log2(e) / sqrt(d) gives the usual softmax). Replaces krn's flash-attention tile program,
  * reference examples/04_libraries/08_flash_attention.py:35-59 (causal mask `where(k_pos <= q_pos, s, -1e30)`;
- * keys past sk are invalid lanes). */
+ * keys past sk are invalid lanes). One head's keys (sk * d * 2 bytes) and queries rounded up to a whole
+ * 256-row tile ((sq + 256) * d * 2 bytes) must each stay under 2 GiB; larger heads are refused with an error. */
 int krn_attention_fwd(int kind, const void* q, const void* k, const void* v, void* o, int64_t bh, int64_t sq,
                       int64_t sk, int64_t d, float scale, int causal, void* stream);
 
