@@ -48,3 +48,30 @@ def test_nn_workspace_query_is_zero_exactly_for_the_products_read_as_they_lie():
     assert query(a, b, 1024, 4096, 4096) == 4096 * 4096 * 2  # 64 tiles: too few for the whole-tile loop
     assert query(a + 8, b, 8192, 8192, 8192) == 8192 * 8192 * 2  # A not 16-byte aligned
     assert query(a, b + 2, 8192, 8192, 8192) == 8192 * 8192 * 2  # B not 16-byte aligned
+
+
+@pytest.mark.skipif(not LIBRARY.exists(), reason="libkrn_amd.so is not built (run __graft_entry__.build())")
+def test_attention_refuses_what_it_cannot_address_before_any_device_call():
+    """krn_attention_fwd checks its arguments on the host and returns -1 with a message before it touches the
+    device: an unknown element kind, a head dimension other than 64 or 128, misaligned tensors, no keys, and heads
+    whose keys (sk * d * 2 bytes) or whose queries rounded up to a whole 256-row tile ((sq + 256) * d * 2 bytes)
+    exceed the 31-bit offsets of its buffer resources."""
+    library = ctypes.CDLL(str(LIBRARY))
+    fwd = library.krn_attention_fwd
+    fwd.restype = ctypes.c_int
+    fwd.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                    ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
+    library.krn_amd_last_error.restype = ctypes.c_char_p
+    p = 1 << 20  # an aligned stand-in address: nothing is dereferenced
+    bf16, f32 = 2, 0
+
+    def refused(*args) -> str:
+        assert fwd(*args) == -1
+        return library.krn_amd_last_error().decode()
+
+    assert "bf16 or f16" in refused(f32, p, p, p, p, 1, 256, 256, 128, 0.1, 1, None)
+    assert "head dimension" in refused(bf16, p, p, p, p, 1, 256, 256, 96, 0.1, 1, None)
+    assert "aligned" in refused(bf16, p + 2, p, p, p, 1, 256, 256, 128, 0.1, 1, None)
+    assert "empty key" in refused(bf16, p, p, p, p, 1, 256, 0, 128, 0.1, 1, None)
+    assert "keys" in refused(bf16, p, p, p, p, 1, 256, 1 << 23, 128, 0.1, 1, None)
+    assert "queries" in refused(bf16, p, p, p, p, 1, (1 << 23) - 256, 256, 128, 0.1, 1, None)
