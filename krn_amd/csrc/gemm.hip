@@ -1801,14 +1801,15 @@ static int launch_mid(const void* a, const void* b, void* c, int64_t m, int64_t 
 }
 
 // 128 x 256 tiles, eight waves (64 x 64 each), for the products between one wave of 128 x 128 tiles and 128 tiles
-// of 256 x 256 (bf16/f16 and int8)
+// of 256 x 256 (bf16/f16 and int8; int8 with three 128-byte stages, 144 KiB: the W8A8 4096 x 14336 x 4096 column
+// tail 49.9 -> 45.2 us against two)
 template <int FMT>
 static int launch_band(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t kbytes, int64_t lda,
                        int64_t ldb, int64_t ldc, const Epilogue& e, hipStream_t stream) {
   if constexpr (FMT == FMT_BF16 || FMT == FMT_F16)
     return launch_pipe<FMT, 128, 256, 2, 4, 4, 64>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   else if constexpr (FMT == FMT_I8)
-    return launch_pipe<FMT, 128, 256, 2, 4, 2, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
+    return launch_pipe<FMT, 128, 256, 2, 4, 3, 128>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
   else
     return launch_gemm<FMT, 128, 128, 2, 2>(a, b, c, m, n, kbytes, lda, ldb, ldc, e, stream);
 }
