@@ -570,35 +570,10 @@ __device__ __forceinline__ void patch_put_t(const V& block, uint32_t* patch, int
 // four blocks are joined into the 32x32 layout of the transposed block and written into the patch transposed.
 // Against the 32x32 direct store (same box, bench legs): bf16 8192^3 equal, fp8 8192^3 0.440 -> 0.424 ms,
 // W8A8 M = 4096 0.272 -> 0.247 ms; write-back instead of non-temporal stores: bf16 1.5 % slower.
-template <bool INT, bool BF, typename V4>
-__device__ __forceinline__ void store16t_direct(const V4 (&acc)[8][8], void* C, int64_t ldc, int64_t row0,
-                                                int64_t col0, const Epilogue& e, int lane) {
+template <bool INT, bool BF, typename V4, typename Ops>
+__device__ __forceinline__ void store16t_direct(const V4 (&acc)[8][8], Ops ops, void* C, int64_t ldc, int64_t row0,
+                                                int64_t col0, int lane) {
   const int r16 = lane & 15, g = lane >> 4;
-  // per operation: the multiplier and addend of a fused multiply-add per row block (row and scalar operations) and
-  // per column of each column block (column operations); the other of the two is the identity x * 1 + (-0), exact
-  // for every x, so each operation is two fused multiply-adds and no selection
-  float rm[DIRECT_OPS][8], ra[DIRECT_OPS][8], cm[DIRECT_OPS][8][4], ca[DIRECT_OPS][8][4];
-#pragma unroll
-  for (int q = 0; q < DIRECT_OPS; ++q) {
-    if (q >= e.nops) break;
-    const int op = e.op[q] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[q] >> VEC_KIND_SHIFT;
-    const bool mul = op < 3, col = op % 3 == 2;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float s = col ? bits_value(kind, vec_bits(e.vec[q], kind, col0 + 16 * j + 4 * g + c)) : 0.0f;
-        cm[q][j][c] = col && mul ? s : 1.0f;
-        ca[q][j][c] = col && !mul ? s : -0.0f;
-      }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float s = col ? 0.0f
-                          : op % 3 == 1 ? bits_value(kind, vec_bits(e.vec[q], kind, row0 + 16 * i + r16)) : e.scalar[q];
-      rm[q][i] = !col && mul ? s : 1.0f;
-      ra[q][i] = !col && !mul ? s : -0.0f;
-    }
-  }
   const uint64_t base = (uint64_t)(static_cast<uint16_t*>(C) + row0 * ldc + col0);
   const uint32_t base_lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
   const uint32_t base_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
@@ -618,13 +593,7 @@ __device__ __forceinline__ void store16t_direct(const V4 (&acc)[8][8], void* C, 
         float v[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) v[c] = INT ? (float)(int32_t)b[c] : (float)b[c];
-#pragma unroll
-        for (int q = 0; q < DIRECT_OPS; ++q) {
-          if (q >= e.nops) break;
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            v[c] = __builtin_fmaf(__builtin_fmaf(v[c], rm[q][i], ra[q][i]), cm[q][j][c], ca[q][j][c]);
-        }
+        ops(v, i, j);
         w[jb][0] = BF ? f2bf2(v[0], v[1]) : ((uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16));
         w[jb][1] = BF ? f2bf2(v[2], v[3]) : ((uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16));
       }
@@ -651,17 +620,110 @@ __device__ __forceinline__ void store16t_direct(const V4 (&acc)[8][8], void* C, 
     }
 }
 
+// The direct store's operations on one block's four values (row 16 i + (lane & 15), columns 16 j + 4 (lane >> 4)
+// + c). Generic: any chain of at most two scalar, row and column multiplies and adds, as two fused multiply-adds
+// each (x * s + (-0) = x * s or x * 1 + s = x + s, and the identity x * 1 + (-0) for the other of the pair: each exact
+// or rounded once, signed zeros included, so the result is the patch path's bit for bit).
+struct Quad16Generic {
+  float rm[DIRECT_OPS][8], ra[DIRECT_OPS][8], cm[DIRECT_OPS][8][4], ca[DIRECT_OPS][8][4];
+  int nops;
+  __device__ void operator()(float (&v)[4], int i, int j) const {
+#pragma unroll
+    for (int q = 0; q < DIRECT_OPS; ++q) {
+      if (q >= nops) break;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        v[c] = __builtin_fmaf(__builtin_fmaf(v[c], rm[q][i], ra[q][i]), cm[q][j][c], ca[q][j][c]);
+    }
+  }
+};
+
+__device__ __forceinline__ void quad16_generic(Quad16Generic& qv, const Epilogue& e, int64_t row0, int64_t col0,
+                                               int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  qv.nops = e.nops;
+  // per operation: the multiplier and addend of a fused multiply-add per row block (row and scalar operations) and
+  // per column of each column block (column operations); the other of the two is the identity x * 1 + (-0), exact
+  // for every x, so each operation is two fused multiply-adds and no selection
+#pragma unroll
+  for (int q = 0; q < DIRECT_OPS; ++q) {
+    if (q >= e.nops) break;
+    const int op = e.op[q] & ((1 << VEC_KIND_SHIFT) - 1), kind = e.op[q] >> VEC_KIND_SHIFT;
+    const bool mul = op < 3, col = op % 3 == 2;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float s = col ? bits_value(kind, vec_bits(e.vec[q], kind, col0 + 16 * j + 4 * g + c)) : 0.0f;
+        qv.cm[q][j][c] = col && mul ? s : 1.0f;
+        qv.ca[q][j][c] = col && !mul ? s : -0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float s = col ? 0.0f
+                          : op % 3 == 1 ? bits_value(kind, vec_bits(e.vec[q], kind, row0 + 16 * i + r16)) : e.scalar[q];
+      qv.rm[q][i] = !col && mul ? s : 1.0f;
+      qv.ra[q][i] = !col && !mul ? s : -0.0f;
+    }
+  }
+}
+
+// W8A8's dequantisation `acc * scale_a[m] * scale_w[n]` (a row multiply, then a column multiply, float32 vectors):
+// the lane's 8 row and 32 column values, fetched before the loop's last slices, and two multiplies per value.
+struct Quad16RowCol {
+  float r[8], c[8][4];
+  __device__ void operator()(float (&v)[4], int i, int j) const {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v[q] = __fmul_rn(__fmul_rn(v[q], r[i]), c[j][q]);
+      // opaque to the compiler, which would otherwise fuse the last multiply into the f16 conversion (a mixed
+      // multiply-add with a +0 addend, rounded once: -0 becomes +0 and the float32 rounding is skipped)
+      asm("" : "+v"(v[q]));
+    }
+  }
+};
+
+__device__ __forceinline__ bool quad16_is_rowcol(const Epilogue& e) {
+  return e.nops == 2 && e.op[0] == MUL_ROW && e.op[1] == MUL_COL;  // kind 0: float32 vectors
+}
+
+__device__ __forceinline__ void quad16_rowcol(Quad16RowCol& rc, const Epilogue& e, int64_t row0, int64_t col0,
+                                              int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  const float* rv = static_cast<const float*>(e.vec[0]);
+  const float* cv = static_cast<const float*>(e.vec[1]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) rc.r[i] = rv[row0 + 16 * i + r16];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) rc.c[j][c] = cv[col0 + 16 * j + 4 * g + c];
+}
+
+// Whether a wave's 128 x 128 region at (row0, col0) takes the direct store.
+__device__ __forceinline__ bool quad16_direct(const Epilogue& e, const void* C, int64_t ldc, int64_t row0,
+                                              int64_t col0, int64_t M, int64_t N) {
+  return direct_epilogue(e) && (ldc % 4) == 0 && (uintptr_t)C % 8 == 0 && row0 + 128 <= M && col0 + 128 <= N &&
+         (int64_t)128 * ldc * 2 <= 0x7fffffff;
+}
+
+// `direct`: quad16_direct of the region; `rowcol`: the epilogue is W8A8's, with its vectors already in `rc`.
 template <bool INT, typename V16, typename V4>
-__device__ __forceinline__ void store_tile16t(const V4 (&acc)[8][8], uint32_t* patch, void* C, int64_t ldc,
+__device__ __forceinline__ void store_tile16t(const V4 (&acc)[8][8], bool direct, bool rowcol,
+                                              const Quad16RowCol& rc, uint32_t* patch, void* C, int64_t ldc,
                                               int64_t row0, int64_t col0, int64_t M, int64_t N, const Epilogue& e,
                                               int lane) {
-  const bool direct = direct_epilogue(e) && (ldc % 4) == 0 && (uintptr_t)C % 8 == 0 && row0 + 128 <= M &&
-                      col0 + 128 <= N && (int64_t)128 * ldc * 2 <= 0x7fffffff;
   if (direct) {
-    if (e.out_kind == BF16)
-      store16t_direct<INT, true>(acc, C, ldc, row0, col0, e, lane);
-    else
-      store16t_direct<INT, false>(acc, C, ldc, row0, col0, e, lane);
+    const bool bf = e.out_kind == BF16;
+    if (rowcol) {
+      if (bf) store16t_direct<INT, true>(acc, rc, C, ldc, row0, col0, lane);
+      else store16t_direct<INT, false>(acc, rc, C, ldc, row0, col0, lane);
+    } else {
+      Quad16Generic qv;
+      quad16_generic(qv, e, row0, col0, lane);
+      if (bf) store16t_direct<INT, true>(acc, qv, C, ldc, row0, col0, lane);
+      else store16t_direct<INT, false>(acc, qv, C, ldc, row0, col0, lane);
+    }
     return;
   }
   const Epilogue local = e;  // taken by address by the out-of-line store
@@ -1326,6 +1388,11 @@ __global__ __launch_bounds__(256, 1) void gemm_quad16(const uint8_t* __restrict_
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) KD_SLICE(u, kt + u);
   }
+  // W8A8's scale vectors go out before the last (up to five) slices, so that their latency runs under MFMAs
+  const int64_t row0 = m0 + wm * 128, col0 = n0 + wn * 128;
+  const bool direct = quad16_direct(e, C, ldc, row0, col0, M, N), rowcol = direct && quad16_is_rowcol(e);
+  Quad16RowCol rc;
+  if (rowcol) quad16_rowcol(rc, e, row0, col0, lane);
 #pragma unroll
   for (int u = 0; u < UNROLL - 1; ++u)
     if (kt + u < nk) KD_SLICE(u, kt + u);
@@ -1346,7 +1413,7 @@ __global__ __launch_bounds__(256, 1) void gemm_quad16(const uint8_t* __restrict_
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   __syncthreads();  // every wave is done with the stages before their LDS becomes the store patches
   uint32_t* patch = reinterpret_cast<uint32_t*>(la0) + wave * PATCH_WORDS;
-  store_tile16t<FMT == FMT_I8, Acc32>(acc, patch, C, ldc, m0 + wm * 128, n0 + wn * 128, M, N, e, lane);
+  store_tile16t<FMT == FMT_I8, Acc32>(acc, direct, rowcol, rc, patch, C, ldc, row0, col0, M, N, e, lane);
 }
 
 // Ping-pong main loop for whole 256 x 256 tiles with 64-byte K slices (bf16/f16: two 32x32x16 steps, int8: two
