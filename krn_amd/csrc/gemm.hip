@@ -707,6 +707,50 @@ __device__ __forceinline__ bool quad16_direct(const Epilogue& e, const void* C, 
          (int64_t)128 * ldc * 2 <= 0x7fffffff;
 }
 
+// 32-bit outputs (int32 from an int8 product with no operations, float32 with at most two scalar, row and column
+// operations) of the transposed blocks: a lane's four values are 16 contiguous bytes of one row, so each block is
+// one 16-byte store per lane (64 bytes of each of 16 rows per instruction), no exchange between lanes.
+__device__ __forceinline__ bool quad16_direct32(const Epilogue& e, const void* C, int64_t ldc, int64_t row0,
+                                                int64_t col0, int64_t M, int64_t N) {
+  bool ops_ok = e.nops <= DIRECT_OPS;
+  for (int i = 0; i < e.nops; ++i) ops_ok &= (e.op[i] & ((1 << VEC_KIND_SHIFT) - 1)) < RELU;
+  const bool kind = (e.out_kind == I32 && e.nops == 0) || (e.out_kind == F32 && ops_ok);
+  return kind && (ldc % 4) == 0 && (uintptr_t)C % 16 == 0 && row0 + 128 <= M && col0 + 128 <= N &&
+         (int64_t)128 * ldc * 4 <= 0x7fffffff;
+}
+
+template <bool INT, typename V4, typename Ops>
+__device__ __forceinline__ void store32t_direct(const V4 (&acc)[8][8], Ops ops, bool raw_int, void* C, int64_t ldc,
+                                                int64_t row0, int64_t col0, int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  const uint64_t base = (uint64_t)(static_cast<uint32_t*>(C) + row0 * ldc + col0);
+  const uint32_t base_lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
+  const uint32_t base_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+  const void* region = (const void*)(((uint64_t)base_hi << 32) | (uint64_t)base_lo);
+  const __amdgpu_buffer_rsrc_t out = panel_rsrc(region, (int64_t)128 * ldc * 4);
+  const uint32_t lane_off = (uint32_t)((r16 * ldc + 4 * g) * 4);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const V4 b = agpr_block(acc[i][j]);
+      u32x4 w;
+      if (INT && raw_int) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) w[c] = (uint32_t)b[c];
+      } else {
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = INT ? (float)(int32_t)b[c] : (float)b[c];
+        ops(v, i, j);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) w[c] = __float_as_uint(v[c]);
+      }
+      const int soff = __builtin_amdgcn_readfirstlane((int)(((int64_t)16 * i * ldc + 16 * j) * 4));
+      __builtin_amdgcn_raw_buffer_store_b128(w, out, (int)lane_off, soff, 2 /* nt */);
+    }
+}
+
 // `direct`: quad16_direct of the region; `rowcol`: the epilogue is W8A8's, with its vectors already in `rc`.
 template <bool INT, typename V16, typename V4>
 __device__ __forceinline__ void store_tile16t(const V4 (&acc)[8][8], bool direct, bool rowcol,
@@ -724,6 +768,12 @@ __device__ __forceinline__ void store_tile16t(const V4 (&acc)[8][8], bool direct
       if (bf) store16t_direct<INT, true>(acc, qv, C, ldc, row0, col0, lane);
       else store16t_direct<INT, false>(acc, qv, C, ldc, row0, col0, lane);
     }
+    return;
+  }
+  if (quad16_direct32(e, C, ldc, row0, col0, M, N)) {
+    Quad16Generic qv;
+    quad16_generic(qv, e, row0, col0, lane);
+    store32t_direct<INT>(acc, qv, e.out_kind == I32, C, ldc, row0, col0, lane);
     return;
   }
   const Epilogue local = e;  // taken by address by the out-of-line store

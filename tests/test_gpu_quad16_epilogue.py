@@ -1,4 +1,4 @@
-"""The four-wave whole-tile loop's direct store with epilogue chains, bit for bit.
+"""The four-wave whole-tile loop's direct stores (16-bit and float32 outputs) with epilogue chains, bit for bit.
 
 gemm_quad16 computes its blocks transposed and stores them straight from the accumulators, applying each operation
 of the chain as fused multiply-adds (x * s + (-0) for a multiply, x * 1 + s for an add, and the identity
@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from krn_amd import T
-from krn_amd.dtypes import BF16, F16, I8
+from krn_amd.dtypes import BF16, F16, F32, I8
 from krn_amd.runtime import library
 from oracle.numerics import bf16_words
 
@@ -51,7 +51,7 @@ CHAINS = [
 ]
 
 
-@pytest.mark.parametrize("out", [BF16, F16])
+@pytest.mark.parametrize("out", [BF16, F16, F32])
 @pytest.mark.parametrize("chain", range(len(CHAINS)))
 def test_direct_store_chain_is_bit_exact(device, chain, out):
     rng = np.random.default_rng(500 + chain)
@@ -78,9 +78,12 @@ def test_direct_store_chain_is_bit_exact(device, chain, out):
         want = want * vals if op in (library.MUL_ROW, library.MUL_COL) else want + vals
         want = want.astype(np.float32)
         ops.append((code, 0.0, vec.pointer))
-    c = device.empty(T.bf16 if out == BF16 else T.f16, M, N)
+    c = device.empty({BF16: T.bf16, F16: T.f16, F32: T.f32}[out], M, N)
     library.gemm_nt(I8, device.to_device(a).pointer, device.to_device(b).pointer, c.pointer, out, M, N, K, ops,
                     device.default_stream.handle)
     got = c.to_host()
+    if out == F32:
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        return
     expect = bf16_words(want) if out == BF16 else want.astype(np.float16).view(np.uint16)
     np.testing.assert_array_equal(got.view(np.uint16), expect)
