@@ -564,9 +564,9 @@ __device__ __forceinline__ void patch_put_t(const V& block, uint32_t* patch, int
 // (two permlane swaps per word), so that each holds 16 contiguous columns of one block and writes them as two
 // 16-byte pieces: per store instruction 64 bytes of each of 16 rows. The untransposed 32x32 layout needs a DPP
 // exchange and three selects per register for whole-line pieces; 8-byte pieces without the exchange were slower
-// (quarter lines). Each epilogue operation is two fused multiply-adds, x * s + (-0) = x * s or x * 1 + s = x + s
-// and the identity x * 1 + (-0), each exact or rounded once, signed zeros included, so the result is the patch
-// path's bit for bit. Everything else (ragged edges, int32 and float32 outputs, activations) goes through the patch:
+// (quarter lines). `ops` applies the epilogue's operations to one block's four values (Quad16Generic,
+// Quad16RowCol below), with the patch path's rounding. 32-bit outputs have their own direct store
+// (store32t_direct); everything else (ragged edges, activations, more than two operations) goes through the patch:
 // four blocks are joined into the 32x32 layout of the transposed block and written into the patch transposed.
 // Against the 32x32 direct store (same box, bench legs): bf16 8192^3 equal, fp8 8192^3 0.440 -> 0.424 ms,
 // W8A8 M = 4096 0.272 -> 0.247 ms; write-back instead of non-temporal stores: bf16 1.5 % slower.
